@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""Benchmark of the GQA decode-attention hot path on one MI355X.
+
+A step is one decode-attention call (bz_gqa_decode through the C ABI) over one batch of synthetic, seeded input
+(breeze-tts-2-flash_amd/workloads.py). The headline workload is config 2 (backbone serving: B2, 16 q / 8 KV heads,
+head_dim 128, capacity 2048, seq_lens 1024); config 3 (KV 4096) is measured in the same run and reported under
+"extra", with the depth frame (config 5) and the ragged batch (config 4).
+
+Timing: W untimed eager calls, then K calls recorded into one HIP graph (torch.cuda.CUDAGraph), replayed once
+untimed and once timed between HIP events recorded on the stream the kernels run on. Cold cache: the K calls
+rotate over enough distinct K/V buffer sets that their valid bytes exceed 640 MB, more than the 256 MB MALL, so
+every call streams its K/V from HBM. value = algorithmic bytes per call / (timed µs per call), in GB/s.
+
+The CPU baseline is the reference's PyTorch CPU attention path (repeat_kv + bf16 matmul + fp32 softmax + matmul,
+models/breeze.py:259-286, as restated in oracle/attention.py:eager_bf16) on the same workload, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+METRIC = "GQA decode-attn µs/call + HBM GB/s (% of peak) at B=2, KV=1024/4096"
+PEAK_HBM_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1000, help="timed calls (K)")
+    p.add_argument("--warmup", type=int, default=50, help="untimed eager calls before the timed region (W)")
+    p.add_argument("--combine", default="auto", choices=["auto", "last_block", "kernel"])
+    p.add_argument("--splits", type=int, default=0, help="0 = library default")
+    p.add_argument("--eager", action="store_true", help="launch each call from Python instead of a HIP graph")
+    p.add_argument("--no-extra", action="store_true", help="headline workload only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--traffic-bytes", type=float, default=None,
+                   help="HBM bytes per call of the split kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE runs")
+    return p.parse_args()
+
+
+def _pkg():
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import __graft_entry__
+    return __graft_entry__.package()
+
+
+def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold):
+    """µs per call for workload w (one q per call) over `steps` calls; cold rotates distinct K/V buffer sets."""
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    g = w.to(dev)
+    read_bytes = workloads.algorithmic_bytes(w.seq_lens.tolist(), w.num_q_heads, w.num_kv_heads, w.head_dim)
+    nsets = max(16, math.ceil(640e6 / read_bytes)) if cold else 1
+    nsets = min(nsets, steps)
+    ks = torch.empty((nsets,) + tuple(g.k.shape), dtype=g.k.dtype, device=dev)
+    vs = torch.empty_like(ks)
+    ks.copy_(g.k.expand_as(ks))
+    vs.copy_(g.v.expand_as(vs))
+    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
+    kw = dict(out=out, combine=combine, num_splits=splits)
+
+    def call(i):
+        pkg.gqa_decode(g.q, ks[i % nsets], vs[i % nsets], g.seq_lens, g.scale, **kw)
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if eager:
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(steps):
+            call(i)
+        end.record(stream)
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                call(i)
+        graph.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / steps
+    # the rotated sets hold identical data: the last call's output must equal a fresh call on set 0
+    ref = pkg.gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, combine=combine, num_splits=splits)
+    torch.cuda.synchronize()
+    if not torch.equal(out.view(torch.int16), ref.view(torch.int16)):
+        raise RuntimeError("benchmark output differs from a direct call")
+    del ks, vs
+    return us, read_bytes, nsets
+
+
+def time_depth_frame(pkg, dev, steps, warmup):
+    """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph."""
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    w = workloads.make(5)
+    g = w.to(dev)
+    nsteps = g.q.shape[0]
+    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
+    frames = max(1, steps // nsteps)
+
+    def frame():
+        for s in range(nsteps):
+            pkg.gqa_decode(g.q[s], g.k, g.v, g.seq_lens[s], g.scale, out=out, max_seq_len=nsteps)
+
+    for _ in range(max(1, warmup // nsteps)):
+        frame()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(frames):
+            frame()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    us_frame = start.elapsed_time(end) * 1000.0 / frames
+    frame_bytes = sum(workloads.algorithmic_bytes([L, L], w.num_q_heads, w.num_kv_heads, w.head_dim)
+                      for L in range(1, nsteps + 1))
+    return us_frame, frame_bytes
+
+
+def cpu_baseline(w, calls=200, warmup=20):
+    """The reference's eager CPU attention on workload w (its StaticCache capacity plus the interval mask, as the
+    reference runs decode), median of `calls` after `warmup`."""
+    import torch
+    from oracle.attention import eager_bf16, interval_mask
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    q = w.q[:, :, None, :]
+    L = int(w.seq_lens[0])
+    mask = interval_mask([0] * w.batch, L - 1, w.capacity)
+    for _ in range(warmup):
+        eager_bf16(q, w.k, w.v, mask, w.scale)
+    ts = []
+    t_end = time.perf_counter() + 30.0
+    for _ in range(calls):
+        t0 = time.perf_counter_ns()
+        eager_bf16(q, w.k, w.v, mask, w.scale)
+        ts.append(time.perf_counter_ns() - t0)
+        if time.perf_counter() > t_end:
+            break
+    return statistics.median(ts) / 1000.0, torch.get_num_threads(), len(ts)
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); the "
+              "decode-attention path is measured at N=1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    pkg = _pkg()
+    from breeze_tts_2_flash_amd import workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    pkg.load()
+
+    w2 = workloads.make(2)
+    splits2 = args.splits or pkg.default_splits(2, 8, 128, w2.capacity, 0)
+    print(f"[bench] config 2 cold, {args.steps} calls, splits={splits2}, combine={args.combine}", file=sys.stderr,
+          flush=True)
+    us, nbytes, nsets = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
+                                   cold=True)
+    gbs = nbytes / us / 1e3
+    print(f"[bench] config 2 cold: {us:.3f} us/call, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+    line = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config 2: backbone decode, B2, 16q/8kv, D128, capacity 2048, seq_lens 1024",
+                   "us_per_call": round(us, 3), "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
+                   "storage": "bf16", "splits": splits2, "combine": args.combine,
+                   "timing": "eager launches" if args.eager else "HIP graph replay, HIP events on the launch stream",
+                   "cache": f"cold: {nsets} rotating K/V sets", "algorithmic_bytes_per_call": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": args.traffic_bytes},
+    }
+    extra = {}
+    if not args.no_extra:
+        us_w, _, _ = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
+                                cold=False)
+        extra["config2_warm"] = {"us_per_call": round(us_w, 3), "GB/s": round(nbytes / us_w / 1e3, 1)}
+        print(f"[bench] config 2 warm: {us_w:.3f} us/call", file=sys.stderr, flush=True)
+        for cfg in (3, 4):
+            w = workloads.make(cfg)
+            us_c, nb, ns = time_calls(pkg, w, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
+                                      cold=True)
+            extra[f"config{cfg}_cold"] = {
+                "workload": workloads.NAMES[cfg], "us_per_call": round(us_c, 3), "GB/s": round(nb / us_c / 1e3, 1),
+                "pct_of_peak_hbm": round(100.0 * nb / us_c / 1e3 / PEAK_HBM_GBS, 1), "bytes": nb, "sets": ns}
+            print(f"[bench] config {cfg} cold: {us_c:.3f} us/call, {nb / us_c / 1e3:.1f} GB/s", file=sys.stderr,
+                  flush=True)
+            del w
+        us_f, fb = time_depth_frame(pkg, dev, args.steps, args.warmup)
+        extra["config5_depth_frame"] = {"us_per_frame": round(us_f, 3), "us_per_call": round(us_f / 32, 3),
+                                        "bytes_per_frame": fb, "GB/s": round(fb / us_f / 1e3, 1)}
+        print(f"[bench] config 5 depth frame: {us_f:.3f} us/frame", file=sys.stderr, flush=True)
+        line["extra"] = extra
+    if not args.no_cpu:
+        us_cpu, cores, n = cpu_baseline(w2)
+        line["cpu_baseline"] = {"value": round(nbytes / us_cpu / 1e3, 3), "unit": "GB/s", "cores": cores,
+                                "kind": "port", "us_per_call": round(us_cpu, 1),
+                                "sample": f"config 2 inputs, eager bf16 chain over capacity 2048 with the interval "
+                                          f"mask, median of {n} calls after 20 warmups"}
+        print(f"[bench] cpu baseline: {us_cpu:.1f} us/call on {cores} threads", file=sys.stderr, flush=True)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,183 @@
+"""GQA flash-decoding attention op: gqa_decode(q, k_cache, v_cache, seq_lens, scale) -> out.
+
+The Python-side op shape the reference's call sites use (flash/csrc/bb_attn.cu:416-418: query, kc, vc, mask,
+scaling, ...), with seq_lens in the mask's place. Every call goes through the C ABI of libbz_gqa_decode.so
+(bz_gqa_decode, include/bz_gqa_decode.h); torch only provides device memory, the current stream and the device
+guard. Workspaces are cached per (device, sizes) like the reference's _workspace (flash/backbone.py:27-37), so a
+call allocates nothing after the first one and can be recorded into a HIP graph.
+
+Errors follow the reference (TORCH_CHECK -> RuntimeError, bb_attn.cu:377-388, :420-447).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from . import kernels
+
+_WS: dict = {}
+_WS_LOCK = threading.Lock()
+
+_COMBINE = {"auto": kernels.COMBINE_AUTO, "last_block": kernels.COMBINE_LAST_BLOCK, "kernel": kernels.COMBINE_KERNEL}
+
+
+def _combine_code(combine) -> int:
+    if isinstance(combine, int):
+        return combine
+    if combine not in _COMBINE:
+        raise RuntimeError(f"combine must be one of {sorted(_COMBINE)}, got {combine!r}")
+    return _COMBINE[combine]
+
+
+def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, capacity: int,
+                    num_splits: int = 0, max_seq_len: int = 0) -> int:
+    """Scratch bytes bz_gqa_decode needs (bz_gqa_decode_workspace_size). num_splits=0 needs a current device."""
+    n = ctypes.c_size_t(0)
+    kernels.check(kernels.load().bz_gqa_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, capacity,
+                                                               num_splits, max_seq_len, ctypes.byref(n)),
+                  "bz_gqa_decode_workspace_size")
+    return int(n.value)
+
+
+def default_splits(batch: int, num_kv_heads: int, head_dim: int, capacity: int, max_seq_len: int = 0) -> int:
+    """Split count the library picks when num_splits=0 (needs a current device for its CU count)."""
+    n = ctypes.c_int32(0)
+    kernels.check(kernels.load().bz_gqa_decode_default_splits(batch, num_kv_heads, head_dim, capacity, max_seq_len,
+                                                               ctypes.byref(n)), "bz_gqa_decode_default_splits")
+    return int(n.value)
+
+
+def get_workspace(device: torch.device, batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                  capacity: int, num_splits: int = 0, max_seq_len: int = 0) -> torch.Tensor:
+    """Zero-initialised, cached scratch for these sizes (the library keeps it zero-ready between calls)."""
+    key = (str(device), batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
+    with _WS_LOCK:
+        ws = _WS.get(key)
+        if ws is None:
+            with torch.cuda.device(device):
+                n = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
+                ws = torch.zeros(n, dtype=torch.uint8, device=device)
+            if ws.data_ptr() % 256:
+                raise RuntimeError("workspace allocation is not 256-byte aligned")
+            _WS[key] = ws
+        return ws
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _q_view(q: torch.Tensor) -> tuple[int, int, int, int, int]:
+    """(B, NH, D, stride_b, stride_h) of a query given as [B, NH, D] or [B, NH, 1, D]."""
+    if q.dim() == 4:
+        _check(q.size(2) == 1, f"query must have q_len == 1, got shape {tuple(q.shape)}")
+        return q.size(0), q.size(1), q.size(3), q.stride(0), q.stride(1)
+    _check(q.dim() == 3, f"query must be [B, NH, D] or [B, NH, 1, D], got shape {tuple(q.shape)}")
+    return q.size(0), q.size(1), q.size(2), q.stride(0), q.stride(1)
+
+
+def _out_view(out: torch.Tensor, B: int, NH: int, D: int) -> tuple[int, int]:
+    """(stride_b, stride_h) of an output given as [B, NH, D], [B, 1, NH, D] (reference layout) or [B, NH, 1, D]."""
+    _check(out.dtype == torch.bfloat16, "out must be bf16")
+    _check(out.stride(-1) == 1, "out's last dimension must be contiguous")
+    if out.dim() == 4 and tuple(out.shape) == (B, 1, NH, D):
+        return out.stride(0), out.stride(2)
+    if out.dim() == 4 and tuple(out.shape) == (B, NH, 1, D):
+        return out.stride(0), out.stride(1)
+    _check(out.dim() == 3 and tuple(out.shape) == (B, NH, D),
+           f"out must be [B, NH, D], [B, 1, NH, D] or [B, NH, 1, D] with B={B}, NH={NH}, D={D}")
+    return out.stride(0), out.stride(1)
+
+
+def _mask_view(mask: torch.Tensor, B: int, cap: int) -> tuple[int, int]:
+    """(bz_mask_dtype, batch stride) of an additive mask [B or 1, 1, 1, >= cap] / [B or 1, >= cap]."""
+    _check(mask.dtype in (torch.bfloat16, torch.float32), "mask dtype must be bf16 or float32")
+    _check(mask.stride(-1) == 1 and mask.size(-1) >= cap, "mask's last dim must be contiguous and >= capacity")
+    _check(all(s == 1 for s in mask.shape[1:-1]), f"mask must be [B or 1, 1, 1, S], got {tuple(mask.shape)}")
+    _check(mask.size(0) in (B, 1), "mask batch dim must be B or 1")
+    code = kernels.MASK_BF16 if mask.dtype == torch.bfloat16 else kernels.MASK_F32
+    return code, (0 if mask.size(0) == 1 else mask.stride(0))
+
+
+def _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine):
+    _check(q.is_cuda, "query must be a device tensor")
+    _check(q.dtype == torch.bfloat16 and k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16,
+           "query, k_cache and v_cache must be bf16")
+    _check(k_cache.device == q.device and v_cache.device == q.device, "all tensors must be on one device")
+    _check(q.stride(-1) == 1, "query's head_dim must be contiguous")
+    B, NH, D, q_sb, q_sh = _q_view(q)
+    _check(k_cache.dim() == 4 and v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+           "k_cache and v_cache must be [B, NKV, capacity, D] with equal shapes and strides")
+    _check(k_cache.size(0) == B and k_cache.size(3) == D and k_cache.stride(3) == 1,
+           f"k_cache {tuple(k_cache.shape)} does not match query {tuple(q.shape)}")
+    NKV, cap = k_cache.size(1), k_cache.size(2)
+    if out is None:
+        out = torch.empty(B, NH, D, dtype=torch.bfloat16, device=q.device)
+    _check(out.device == q.device, "out must be on the query's device")
+    o_sb, o_sh = _out_view(out, B, NH, D)
+    a = kernels.GqaDecodeArgs()
+    a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q_sb, q_sh
+    a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    a.kv_stride_b, a.kv_stride_h, a.kv_stride_s = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.scale = float(scale)
+    a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), o_sb, o_sh
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity = B, NH, NKV, D, cap
+    a.num_splits, a.max_seq_len, a.combine = int(num_splits), int(max_seq_len), _combine_code(combine)
+    return a, out
+
+
+def _int32_rows(t: torch.Tensor, B: int, name: str, device) -> torch.Tensor:
+    _check(t.dtype == torch.int32 and t.device == device and t.numel() == B and t.is_contiguous(),
+           f"{name} must be a contiguous int32 device tensor of {B} elements")
+    return t
+
+
+def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
+               scale: float, out: torch.Tensor | None = None, *, kv_start: torch.Tensor | None = None,
+               mask: torch.Tensor | None = None, num_splits: int = 0, max_seq_len: int = 0,
+               combine: str | int = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """GQA decode attention over [kv_start[b], seq_lens[b]) of a bf16 KV cache.
+
+    q: [B, NH, D] or [B, NH, 1, D] bf16 (head_dim contiguous); k_cache, v_cache: [B, NKV, capacity, D] bf16;
+    seq_lens: [B] int32 (exclusive end); kv_start: [B] int32 or None; mask: optional additive mask
+    [B or 1, 1, 1, >= capacity] (bf16 or fp32) applied inside the range (<= -1e30 excludes a position);
+    out: [B, NH, D] (default), [B, 1, NH, D] or [B, NH, 1, D] bf16. Returns out.
+    """
+    a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
+    dev = q.device
+    a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
+    a.kv_start = _int32_rows(kv_start, a.batch, "kv_start", dev).data_ptr() if kv_start is not None else None
+    if mask is not None:
+        _check(mask.device == dev, "mask must be on the query's device")
+        a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
+        a.mask = mask.data_ptr()
+    with torch.cuda.device(dev):
+        ws = workspace if workspace is not None else get_workspace(
+            dev, a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity, a.num_splits, a.max_seq_len)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        kernels.check(kernels.load().bz_gqa_decode(ctypes.byref(a), ctypes.c_void_p(stream)), "bz_gqa_decode")
+    return out
+
+
+def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, mask: torch.Tensor,
+                      scale: float, out: torch.Tensor | None = None, *, num_splits: int = 0, max_seq_len: int = 0,
+                      combine: str | int = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Interval-mask form (bz_gqa_decode_masked): each row's range is the first..last position with mask > -1e30,
+    derived on the device; the mask is added inside that range. Same shapes as gqa_decode."""
+    a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
+    dev = q.device
+    _check(mask.device == dev, "mask must be on the query's device")
+    a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
+    a.mask = mask.data_ptr()
+    with torch.cuda.device(dev):
+        ws = workspace if workspace is not None else get_workspace(
+            dev, a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity, a.num_splits, a.max_seq_len)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        kernels.check(kernels.load().bz_gqa_decode_masked(ctypes.byref(a), ctypes.c_void_p(stream)),
+                      "bz_gqa_decode_masked")
+    return out

@@ -1,0 +1,704 @@
+// GQA flash-decoding attention for one decode step (q_len == 1) against a bf16 KV cache, written for gfx950
+// (MI355X, CDNA4: wave64, 256 CUs in 8 XCDs, HBM3E).
+//
+// What it computes is the reference's decode attention (flash/csrc/bb_attn.cu:1-17, the eager chain of
+// third_party/breeze-tts/models/breeze.py:259-286 with the head map of repeat_kv, :245-256): for each row b and
+// q head h, softmax(scale * q . K^T + mask) . V over the KV positions [kv_start[b], seq_lens[b]) of KV head
+// h / G. The arithmetic is fp32 throughout (the north-star oracle), not the reference's bf16 rounding chain.
+//
+// Work decomposition (split-K over the KV length, "flash-decoding"):
+//   grid (splits, num_kv_heads, batch), 256 threads = 4 wave64 per workgroup.
+//   Each row's valid length is cut on the device into nact <= splits chunks of
+//   chunk = max(min_chunk, ceil(len / splits)) positions, so a fixed grid serves every length (HIP-graph safe) and
+//   the work follows the real length: workgroups past nact exit at once.
+//   A workgroup streams its chunk in tiles of ROWS * PPT positions. A KV row of head_dim bf16 is read by
+//   LPR = head_dim / 8 consecutive lanes, 16 bytes each, so one wave64 load instruction covers 64 * 16 B of
+//   consecutive positions (fully coalesced) and every K/V byte is read once, by one lane, straight into VGPRs.
+//   All G q heads of the GQA group use the same K/V registers.
+//   q . k: 8 fp32 FMAs per lane, then a 16- (or 8-) lane sum with DPP row permutations (no LDS traffic).
+//   Softmax: online, base 2 (scale * log2(e) folded into q), one running (max, sum, acc) per 16-lane row, so the
+//   main loop has no cross-row communication. Rows are merged at the end (xor shuffles inside the wave, LDS across
+//   the 4 waves) with the log-sum-exp rule.
+//   One split (nact == 1): the workgroup writes the bf16 output directly.
+//   Several splits: each writes (acc[D], max, sum) in fp32 to the workspace; they are merged in split order either
+//   by the last workgroup of the (batch, kv head) to finish (atomic counter, one launch) or by a second kernel.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include <atomic>
+
+#include "bz_gqa_decode.h"
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 wave64
+constexpr int kWave = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxSplits = 256;
+constexpr int kMaxDevices = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kExcluded = -1e30f;  // mask values <= this exclude the position (bb_attn.cu:9-11, :115)
+
+struct Params {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_sb, kv_sh, kv_ss;
+  const int32_t* seq_lens;
+  const int32_t* kv_start;
+  const void* mask;
+  int64_t m_sb;
+  float scale_log2;  // scale * log2(e)
+  uint16_t* out;
+  int64_t o_sb, o_sh;
+  int B, NH, NKV, cap, splits, min_chunk;
+  int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
+  float* part_acc;   // [B, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
+  float2* part_ml;   // [B, NH, splits]     (m, sum_p 2^(s_p - m))
+  int* counters;     // [B, NKV]            arrivals, reset by the merging workgroup
+};
+
+// ---------------------------------------------------------------------------------------------- helpers
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& w, float f[8]) {
+  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over the LPR (8 or 16) consecutive lanes that hold one KV row; every lane of the row gets the same value
+// (each step adds a lane-permuted copy, and fp32 addition is commutative, so all lanes agree bit for bit).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+  static_assert(LPR == 8 || LPR == 16, "row_sum covers 8 or 16 lanes");
+  x += dpp<0xb1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4e>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within each 8 lanes
+  if (LPR == 16) x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i within each 16 lanes
+  return x;
+}
+
+// Clamp the row's range so that no access can leave [0, capacity).
+__device__ __forceinline__ void row_range(const Params& p, int b, int& start, int& end) {
+  int e = p.seq_lens[b];
+  e = e < 0 ? 0 : (e > p.cap ? p.cap : e);
+  int s = p.kv_start ? p.kv_start[b] : 0;
+  s = s < 0 ? 0 : (s > e ? e : s);
+  start = s;
+  end = e;
+}
+
+// Positions per split and number of non-empty splits for a row of length len (>= 1 split even when empty, so
+// that someone writes the row's output).
+__device__ __forceinline__ int split_chunk(int len, int splits, int min_chunk) {
+  const int c = (len + splits - 1) / splits;
+  return c > min_chunk ? c : min_chunk;
+}
+__device__ __forceinline__ int split_count(int len, int chunk) { return len > 0 ? (len + chunk - 1) / chunk : 1; }
+
+template <int MK>
+__device__ __forceinline__ float load_mask(const void* m, int64_t off) {
+  if (MK == BZ_MASK_BF16) return bf16_to_f32(static_cast<const uint16_t*>(m)[off]);
+  return static_cast<const float*>(m)[off];
+}
+
+// Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
+template <int D, int G>
+__device__ void merge_splits(const Params& p, int b, int h, int nact) {
+  __shared__ float s_w[G][kMaxSplits];  // split maxima, then per-split weights 2^(m_s - M)
+  __shared__ float s_l[G][kMaxSplits];  // split sums
+  __shared__ float s_inv[G];            // 1 / sum_s w_s l_s
+  const int tid = threadIdx.x;
+  for (int o = tid; o < G * nact; o += kThreads) {
+    const int g = o / nact, s = o % nact;
+    const float2 ml = p.part_ml[((int64_t)b * p.NH + h * G + g) * p.splits + s];
+    s_w[g][s] = ml.x;
+    s_l[g][s] = ml.y;
+  }
+  __syncthreads();
+  if (tid < G) {
+    const int g = tid;
+    float M = -INFINITY;
+    for (int s = 0; s < nact; ++s) M = fmaxf(M, s_w[g][s]);
+    const float mu = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+    for (int s = 0; s < nact; ++s) {
+      const float w = fast_exp2(s_w[g][s] - mu);
+      s_w[g][s] = w;
+      L = fmaf(w, s_l[g][s], L);
+    }
+    s_inv[g] = L > 0.f ? 1.f / L : 0.f;
+  }
+  __syncthreads();
+  for (int o = tid; o < G * D; o += kThreads) {
+    const int g = o / D, d = o % D, hq = h * G + g;
+    const float* pa = p.part_acc + ((int64_t)b * p.NH + hq) * p.splits * D + d;
+    float a = 0.f;
+    int s = 0;
+    for (; s + 8 <= nact; s += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = pa[(int64_t)(s + u) * D];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a = fmaf(s_w[g][s + u], t[u], a);
+    }
+    for (; s < nact; ++s) a = fmaf(s_w[g][s], pa[(int64_t)s * D], a);
+    p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(a * s_inv[g]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- kernels
+
+template <int D, int G, int PPT, int MK>
+__global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
+  constexpr int LPR = D / 8;            // lanes per KV row, 16 B (8 bf16) each
+  constexpr int ROWS = kThreads / LPR;  // KV rows per load instruction across the workgroup
+  constexpr int TP = ROWS * PPT;        // positions per tile
+  constexpr int RPW = kWave / LPR;      // rows per wave
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
+
+  int start, end;
+  row_range(p, b, start, end);
+  const int len = end - start;
+  const int chunk = split_chunk(len, p.splits, p.min_chunk);
+  const int nact = split_count(len, chunk);
+  if (split >= nact) return;
+  const int lo = start + split * chunk;
+  const int hi = min(lo + chunk, end);
+
+  // q of the G heads of this group, this lane's 8 dims, scaled by scale * log2(e)
+  float qf[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + 8 * c;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qf[g][j] = bf16_to_f32(qp[j]) * p.scale_log2;
+  }
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
+  }
+
+  const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + 8 * c;
+  const uint16_t* kb = p.k + head_off;
+  const uint16_t* vb = p.v + head_off;
+  const int64_t mrow = (int64_t)b * p.m_sb;
+
+  for (int t0 = lo; t0 < hi; t0 += TP) {
+    uint4 kr[PPT], vr[PPT];
+    float mv[PPT];
+    // issue every K and V load of the tile before any arithmetic
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pos = t0 + r + ROWS * i;
+      if (pos < hi) {
+        kr[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)pos * p.kv_ss);
+        vr[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)pos * p.kv_ss);
+      } else {
+        kr[i] = make_uint4(0, 0, 0, 0);
+        vr[i] = make_uint4(0, 0, 0, 0);
+      }
+      if (MK != BZ_MASK_NONE) mv[i] = (pos < hi) ? load_mask<MK>(p.mask, mrow + pos) : 0.f;
+    }
+
+    float s[G][PPT];
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pos = t0 + r + ROWS * i;
+      float kf[8];
+      unpack8(kr[i], kf);
+      bool inc = pos < hi;
+      if (MK != BZ_MASK_NONE) {
+        inc = inc && (mv[i] > kExcluded);
+        // an excluded position must not touch the accumulator even through 0 * V (V may hold NaN there)
+        if (!inc) vr[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d = fmaf(qf[g][j], kf[j], d);
+        d = row_sum<LPR>(d);
+        if (MK != BZ_MASK_NONE) d = fmaf(mv[i], kLog2e, d);
+        s[g][i] = inc ? d : -INFINITY;
+      }
+    }
+
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mt = s[g][0];
+#pragma unroll
+      for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
+      const float mn = fmaxf(m[g], mt);
+      const float mu = (mn == -INFINITY) ? 0.f : mn;
+      const float alpha = fast_exp2(m[g] - mu);
+      l[g] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        s[g][i] = fast_exp2(s[g][i] - mu);
+        l[g] += s[g][i];
+      }
+      m[g] = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      float vf[8];
+      unpack8(vr[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
+    }
+  }
+
+  // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims)
+#pragma unroll
+  for (int off = LPR; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo2 = __shfl_xor(l[g], off);
+      const float mn = fmaxf(m[g], mo);
+      const float mu = (mn == -INFINITY) ? 0.f : mn;
+      const float a = fast_exp2(m[g] - mu), bo = fast_exp2(mo - mu);
+      l[g] = l[g] * a + lo2 * bo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] = acc[g][j] * a + __shfl_xor(acc[g][j], off) * bo;
+      m[g] = mn;
+    }
+  }
+
+  // merge the 4 waves through LDS
+  __shared__ float s_acc[kWaves][G][D];
+  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
+  const int w = tid / kWave, lane = tid % kWave;
+  if (lane < LPR) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_acc[w][g][8 * c + j] = acc[g][j];
+      if (lane == 0) {
+        s_m[w][g] = m[g];
+        s_l[w][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  (void)RPW;
+
+  for (int o = tid; o < G * D; o += kThreads) {
+    const int g = o / D, d = o % D, hq = h * G + g;
+    float M = s_m[0][g];
+#pragma unroll
+    for (int u = 1; u < kWaves; ++u) M = fmaxf(M, s_m[u][g]);
+    const float mu = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int u = 0; u < kWaves; ++u) {
+      const float e = fast_exp2(s_m[u][g] - mu);
+      L = fmaf(e, s_l[u][g], L);
+      A = fmaf(e, s_acc[u][g][d], A);
+    }
+    if (nact == 1) {
+      p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(L > 0.f ? A / L : 0.f);
+    } else {
+      const int64_t ps = ((int64_t)b * p.NH + hq) * p.splits + split;
+      p.part_acc[ps * D + d] = A;
+      if (d == 0) p.part_ml[ps] = make_float2(M, L);
+    }
+  }
+  if (nact == 1 || !p.combine_last) return;
+
+  // last-arriving workgroup of this (b, kv head) merges the splits
+  __shared__ int s_last;
+  __threadfence();  // release this workgroup's partials at device scope
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&p.counters[b * p.NKV + h], 1);
+    s_last = (prev == nact - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();  // acquire the other workgroups' partials
+  if (tid == 0) p.counters[b * p.NKV + h] = 0;
+  merge_splits<D, G>(p, b, h, nact);
+}
+
+// Second-launch merge: one workgroup per (kv head, row).
+template <int D, int G>
+__global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  int start, end;
+  row_range(p, b, start, end);
+  const int len = end - start;
+  const int nact = split_count(len, split_chunk(len, p.splits, p.min_chunk));
+  if (nact == 1) return;  // the split kernel wrote the output
+  merge_splits<D, G>(p, b, h, nact);
+}
+
+// Interval of the additive mask row: first and last position with value > -1e30.
+template <int MK>
+__global__ void __launch_bounds__(kThreads) mask_range_kernel(const void* mask, int64_t m_sb, int cap,
+                                                              int32_t* start, int32_t* end) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  int lo = cap, hi = -1;
+  for (int pos = tid; pos < cap; pos += kThreads) {
+    if (load_mask<MK>(mask, (int64_t)b * m_sb + pos) > kExcluded) {
+      lo = min(lo, pos);
+      hi = max(hi, pos);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    lo = min(lo, __shfl_xor(lo, off));
+    hi = max(hi, __shfl_xor(hi, off));
+  }
+  __shared__ int s_lo[kWaves], s_hi[kWaves];
+  if (tid % kWave == 0) {
+    s_lo[tid / kWave] = lo;
+    s_hi[tid / kWave] = hi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int u = 1; u < kWaves; ++u) {
+      lo = min(lo, s_lo[u]);
+      hi = max(hi, s_hi[u]);
+    }
+    const bool any = hi >= 0;
+    start[b] = any ? lo : 0;
+    end[b] = any ? hi + 1 : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- host side
+
+using SplitFn = void (*)(const Params);
+
+template <int D, int G, int MK>
+SplitFn pick_ppt(int ppt) {
+  switch (ppt) {
+    case 1: return gqa_split_kernel<D, G, 1, MK>;
+    case 2: return gqa_split_kernel<D, G, 2, MK>;
+    case 4: return gqa_split_kernel<D, G, 4, MK>;
+    default: return gqa_split_kernel<D, G, 8, MK>;
+  }
+}
+
+template <int D, int G>
+SplitFn pick_mask(int mk, int ppt) {
+  switch (mk) {
+    case BZ_MASK_BF16: return pick_ppt<D, G, BZ_MASK_BF16>(ppt);
+    case BZ_MASK_F32: return pick_ppt<D, G, BZ_MASK_F32>(ppt);
+    default: return pick_ppt<D, G, BZ_MASK_NONE>(ppt);
+  }
+}
+
+template <int D>
+SplitFn pick_group(int G, int mk, int ppt) {
+  switch (G) {
+    case 1: return pick_mask<D, 1>(mk, ppt);
+    case 2: return pick_mask<D, 2>(mk, ppt);
+    case 4: return pick_mask<D, 4>(mk, ppt);
+    case 8: return pick_mask<D, 8>(mk, ppt);
+    default: return nullptr;
+  }
+}
+
+SplitFn pick_split(int D, int G, int mk, int ppt) {
+  if (D == 128) return pick_group<128>(G, mk, ppt);
+  if (D == 64) return pick_group<64>(G, mk, ppt);
+  return nullptr;
+}
+
+SplitFn pick_combine(int D, int G) {
+#define BZ_COMBINE_CASE(DD, GG) \
+  if (D == DD && G == GG) return gqa_combine_kernel<DD, GG>;
+  BZ_COMBINE_CASE(128, 1) BZ_COMBINE_CASE(128, 2) BZ_COMBINE_CASE(128, 4) BZ_COMBINE_CASE(128, 8)
+  BZ_COMBINE_CASE(64, 1) BZ_COMBINE_CASE(64, 2) BZ_COMBINE_CASE(64, 4) BZ_COMBINE_CASE(64, 8)
+#undef BZ_COMBINE_CASE
+  return nullptr;
+}
+
+bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
+bool supported_dim(int D) { return D == 64 || D == 128; }
+
+// Smallest chunk a split gets: 16 KB of K+V (32 positions at head_dim 128, 64 at head_dim 64).
+int min_chunk_for(int D) { return (16 * 1024) / (4 * D); }
+
+// Positions per thread per tile: the smallest power of two whose tile covers the expected chunk, capped so that
+// the K/V registers (2 * PPT * 4 VGPRs) plus q and the accumulators (16 * G VGPRs) stay in budget.
+int ppt_for(int D, int G, int chunk) {
+  const int rows = kThreads / (D / 8);
+  int cap = 8;
+  if (G >= 8) cap = 2;
+  else if (G >= 4) cap = 4;
+  int ppt = 1;
+  while (ppt < cap && rows * ppt < chunk) ppt <<= 1;
+  return ppt;
+}
+
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int device_cus(int* cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return BZ_ERR_DEVICE;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int cached = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (cached > 0) {
+      *cus = cached;
+      return BZ_OK;
+    }
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return BZ_ERR_DEVICE;
+  if (dev >= 0 && dev < kMaxDevices) g_cu_count[dev].store(n, std::memory_order_relaxed);
+  *cus = n;
+  return BZ_OK;
+}
+
+int effective_len(int capacity, int max_seq_len) {
+  return (max_seq_len > 0 && max_seq_len < capacity) ? max_seq_len : capacity;
+}
+
+int default_splits_for(int units, int D, int len, int cus) {
+  const int min_chunk = min_chunk_for(D);
+  const int useful = len > 0 ? (len + min_chunk - 1) / min_chunk : 1;
+  const int target = 2 * cus;  // two workgroups per CU
+  int s = (target + units - 1) / units;
+  if (s > useful) s = useful;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return s < 1 ? 1 : s;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct WsLayout {
+  size_t acc, ml, counters, ranges, total;
+};
+
+WsLayout ws_layout(int B, int NH, int NKV, int D, int splits) {
+  WsLayout w;
+  w.acc = 0;
+  w.ml = align256(w.acc + (size_t)B * NH * splits * D * sizeof(float));
+  w.counters = align256(w.ml + (size_t)B * NH * splits * sizeof(float2));
+  w.ranges = align256(w.counters + (size_t)B * NKV * sizeof(int));
+  w.total = align256(w.ranges + (size_t)2 * B * sizeof(int32_t));
+  return w;
+}
+
+int check_sizes(int B, int NH, int NKV, int D, int cap) {
+  if (B <= 0 || NH <= 0 || NKV <= 0 || cap <= 0 || D <= 0) return BZ_ERR_SHAPE;
+  if (NH % NKV != 0) return BZ_ERR_SHAPE;
+  if (B > 65535 || NKV > 65535) return BZ_ERR_SHAPE;  // grid.z / grid.y limits
+  if (!supported_dim(D) || !supported_group(NH / NKV)) return BZ_ERR_UNSUPPORTED;
+  return BZ_OK;
+}
+
+int resolve_splits(const bz_gqa_decode_args* a, int* splits) {
+  if (a->num_splits < 0 || a->num_splits > kMaxSplits) return BZ_ERR_SHAPE;
+  if (a->num_splits > 0) {
+    *splits = a->num_splits;
+    return BZ_OK;
+  }
+  int cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc != BZ_OK) return rc;
+  *splits = default_splits_for(a->batch * a->num_kv_heads, a->head_dim,
+                               effective_len(a->capacity, a->max_seq_len), cus);
+  return BZ_OK;
+}
+
+int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
+           int mask_kind) {
+  const int B = a->batch, NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
+  const int G = NH / NKV;
+  int splits = 0;
+  int rc = resolve_splits(a, &splits);
+  if (rc != BZ_OK) return rc;
+  if (a->combine < BZ_COMBINE_AUTO || a->combine > BZ_COMBINE_KERNEL) return BZ_ERR_COMBINE_MODE;
+  const WsLayout ws = ws_layout(B, NH, NKV, D, splits);
+  if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
+
+  const int min_chunk = min_chunk_for(D);
+  const int len = effective_len(cap, a->max_seq_len);
+  int chunk = (len + splits - 1) / splits;
+  if (chunk < min_chunk) chunk = min_chunk;
+  const int ppt = ppt_for(D, G, chunk);
+  SplitFn split_fn = pick_split(D, G, mask_kind, ppt);
+  SplitFn comb_fn = pick_combine(D, G);
+  if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
+
+  char* wsb = static_cast<char*>(a->workspace);
+  Params p;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.q_sb = a->q_stride_b;
+  p.q_sh = a->q_stride_h;
+  p.k = static_cast<const uint16_t*>(a->k_cache);
+  p.v = static_cast<const uint16_t*>(a->v_cache);
+  p.kv_sb = a->kv_stride_b;
+  p.kv_sh = a->kv_stride_h;
+  p.kv_ss = a->kv_stride_s;
+  p.seq_lens = seq_lens;
+  p.kv_start = kv_start;
+  p.mask = a->mask;
+  p.m_sb = a->mask_stride_b;
+  p.scale_log2 = a->scale * kLog2e;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.o_sb = a->out_stride_b;
+  p.o_sh = a->out_stride_h;
+  p.B = B;
+  p.NH = NH;
+  p.NKV = NKV;
+  p.cap = cap;
+  p.splits = splits;
+  p.min_chunk = min_chunk;
+  const bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
+  p.combine_last = two_kernels ? 0 : 1;
+  p.part_acc = reinterpret_cast<float*>(wsb + ws.acc);
+  p.part_ml = reinterpret_cast<float2*>(wsb + ws.ml);
+  p.counters = reinterpret_cast<int*>(wsb + ws.counters);
+
+  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, B), dim3(kThreads), 0, stream, p);
+  if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
+  if (two_kernels && splits > 1) {
+    hipLaunchKernelGGL(comb_fn, dim3(NKV, B), dim3(kThreads), 0, stream, p);
+    if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
+  }
+  return BZ_OK;
+}
+
+int check_common(const bz_gqa_decode_args* a) {
+  if (a == nullptr) return BZ_ERR_NULL;
+  if (a->q == nullptr || a->k_cache == nullptr || a->v_cache == nullptr || a->out == nullptr) return BZ_ERR_NULL;
+  int rc = check_sizes(a->batch, a->num_q_heads, a->num_kv_heads, a->head_dim, a->capacity);
+  if (rc != BZ_OK) return rc;
+  const uintptr_t kp = reinterpret_cast<uintptr_t>(a->k_cache), vp = reinterpret_cast<uintptr_t>(a->v_cache);
+  if ((kp | vp) & 15) return BZ_ERR_ALIGNMENT;
+  if ((a->kv_stride_b | a->kv_stride_h | a->kv_stride_s) & 7) return BZ_ERR_ALIGNMENT;
+  if (a->kv_stride_s < a->head_dim) return BZ_ERR_SHAPE;
+  if (a->mask_dtype < BZ_MASK_NONE || a->mask_dtype > BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  return BZ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int bz_gqa_decode(const bz_gqa_decode_args* a, hipStream_t stream) {
+  int rc = check_common(a);
+  if (rc != BZ_OK) return rc;
+  if (a->seq_lens == nullptr) return BZ_ERR_NULL;
+  const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
+  if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
+  return launch(a, stream, a->seq_lens, a->kv_start, mk);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_masked(const bz_gqa_decode_args* a, hipStream_t stream) {
+  int rc = check_common(a);
+  if (rc != BZ_OK) return rc;
+  if (a->mask == nullptr) return BZ_ERR_NULL;
+  if (a->mask_dtype != BZ_MASK_BF16 && a->mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  int splits = 0;
+  rc = resolve_splits(a, &splits);
+  if (rc != BZ_OK) return rc;
+  const WsLayout ws = ws_layout(a->batch, a->num_q_heads, a->num_kv_heads, a->head_dim, splits);
+  if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
+  int32_t* ranges = reinterpret_cast<int32_t*>(static_cast<char*>(a->workspace) + ws.ranges);
+  int32_t* start = ranges;
+  int32_t* end = ranges + a->batch;
+  if (a->mask_dtype == BZ_MASK_BF16)
+    hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_BF16>, dim3(a->batch), dim3(kThreads), 0, stream, a->mask,
+                       a->mask_stride_b, a->capacity, start, end);
+  else
+    hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_F32>, dim3(a->batch), dim3(kThreads), 0, stream, a->mask,
+                       a->mask_stride_b, a->capacity, start, end);
+  if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
+  return launch(a, stream, end, start, a->mask_dtype);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_workspace_size(int32_t batch, int32_t num_q_heads,
+                                                                        int32_t num_kv_heads, int32_t head_dim,
+                                                                        int32_t capacity, int32_t num_splits,
+                                                                        int32_t max_seq_len, size_t* bytes) {
+  if (bytes == nullptr) return BZ_ERR_NULL;
+  int rc = check_sizes(batch, num_q_heads, num_kv_heads, head_dim, capacity);
+  if (rc != BZ_OK) return rc;
+  if (num_splits < 0 || num_splits > kMaxSplits) return BZ_ERR_SHAPE;
+  int splits = num_splits;
+  if (splits == 0) {
+    int cus = 0;
+    rc = device_cus(&cus);
+    if (rc != BZ_OK) return rc;
+    splits = default_splits_for(batch * num_kv_heads, head_dim, effective_len(capacity, max_seq_len), cus);
+  }
+  *bytes = ws_layout(batch, num_q_heads, num_kv_heads, head_dim, splits).total;
+  return BZ_OK;
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_default_splits(int32_t batch, int32_t num_kv_heads,
+                                                                        int32_t head_dim, int32_t capacity,
+                                                                        int32_t max_seq_len, int32_t* num_splits) {
+  if (num_splits == nullptr) return BZ_ERR_NULL;
+  if (batch <= 0 || num_kv_heads <= 0 || capacity <= 0) return BZ_ERR_SHAPE;
+  if (!supported_dim(head_dim)) return BZ_ERR_UNSUPPORTED;
+  int cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc != BZ_OK) return rc;
+  *num_splits = default_splits_for(batch * num_kv_heads, head_dim, effective_len(capacity, max_seq_len), cus);
+  return BZ_OK;
+}
+
+__attribute__((visibility("default"))) const char* bz_status_string(int status) {
+  switch (status) {
+    case BZ_OK: return "ok";
+    case BZ_ERR_NULL: return "a required pointer is NULL";
+    case BZ_ERR_SHAPE: return "a size is out of range (or num_q_heads is not a multiple of num_kv_heads)";
+    case BZ_ERR_UNSUPPORTED: return "unsupported head_dim (64, 128) or GQA group size (1, 2, 4, 8)";
+    case BZ_ERR_ALIGNMENT: return "K/V pointers and strides must be 16-byte aligned, workspace 256-byte aligned";
+    case BZ_ERR_WORKSPACE: return "workspace missing or smaller than bz_gqa_decode_workspace_size()";
+    case BZ_ERR_MASK_DTYPE: return "mask_dtype must be BZ_MASK_BF16 or BZ_MASK_F32 when a mask is given";
+    case BZ_ERR_LAUNCH: return "kernel launch failed";
+    case BZ_ERR_DEVICE: return "HIP device query failed";
+    case BZ_ERR_COMBINE_MODE: return "combine must be BZ_COMBINE_AUTO, _LAST_BLOCK or _KERNEL";
+    default: return "unknown status";
+  }
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_abi_version(void) { return BZ_GQA_DECODE_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,128 @@
+"""Build and load the HIP library libbz_gqa_decode.so (the C ABI in include/bz_gqa_decode.h).
+
+Counterpart of the reference's extension loader (flash/kernels.py:20-87): the reference JIT-builds a pybind
+extension with nvcc under a process lock and caches it. Here hipcc builds one plain shared library for gfx950,
+in-tree next to this file, ahead of time (build()); load() only opens it, under a lock, once per process, and
+declares the C signatures for ctypes. There is no fallback: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import shutil
+import subprocess
+import threading
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+REPO_DIR = PKG_DIR.parent
+INCLUDE = REPO_DIR / "include"
+LIB_NAME = "libbz_gqa_decode.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+SOURCES = ["gqa_decode.hip"]
+ARCH = "gfx950"
+# -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32)
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+ABI_VERSION = 1
+
+# exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
+EXPORTS = (
+    "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_workspace_size", "bz_gqa_decode_default_splits",
+    "bz_status_string", "bz_gqa_decode_abi_version",
+)
+
+MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
+COMBINE_AUTO, COMBINE_LAST_BLOCK, COMBINE_KERNEL = 0, 1, 2
+
+
+class GqaDecodeArgs(ctypes.Structure):
+    """Mirror of struct bz_gqa_decode_args (field order, types and C alignment)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride_b", ctypes.c_int64), ("q_stride_h", ctypes.c_int64),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("kv_stride_b", ctypes.c_int64), ("kv_stride_h", ctypes.c_int64), ("kv_stride_s", ctypes.c_int64),
+        ("seq_lens", ctypes.c_void_p), ("kv_start", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p), ("mask_dtype", ctypes.c_int32), ("mask_stride_b", ctypes.c_int64),
+        ("scale", ctypes.c_float),
+        ("out", ctypes.c_void_p), ("out_stride_b", ctypes.c_int64), ("out_stride_h", ctypes.c_int64),
+        ("batch", ctypes.c_int32), ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("capacity", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32), ("max_seq_len", ctypes.c_int32), ("combine", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_LOCK = threading.Lock()
+_LIB = None
+
+
+def hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libbz_gqa_decode.so)")
+
+
+def build_command(out: Path = LIB_PATH) -> list[str]:
+    return [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", str(out), *[str(CSRC / s) for s in SOURCES]]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile libbz_gqa_decode.so for gfx950 in-tree (always recompiles). Returns its path."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = build_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+    os.replace(tmp, LIB_PATH)  # atomic: a concurrent load() sees the old or the new library, never half of one
+    return LIB_PATH
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    P = ctypes.POINTER
+    lib.bz_gqa_decode.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p]
+    lib.bz_gqa_decode.restype = ctypes.c_int
+    lib.bz_gqa_decode_masked.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p]
+    lib.bz_gqa_decode_masked.restype = ctypes.c_int
+    lib.bz_gqa_decode_workspace_size.argtypes = [ctypes.c_int32] * 7 + [P(ctypes.c_size_t)]
+    lib.bz_gqa_decode_workspace_size.restype = ctypes.c_int
+    lib.bz_gqa_decode_default_splits.argtypes = [ctypes.c_int32] * 5 + [P(ctypes.c_int32)]
+    lib.bz_gqa_decode_default_splits.restype = ctypes.c_int
+    lib.bz_status_string.argtypes = [ctypes.c_int]
+    lib.bz_status_string.restype = ctypes.c_char_p
+    lib.bz_gqa_decode_abi_version.argtypes = []
+    lib.bz_gqa_decode_abi_version.restype = ctypes.c_int
+
+
+def load() -> ctypes.CDLL:
+    """Open the built library once per process (thread-safe). Raises if it has not been built."""
+    global _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; "
+                               "g.build()'); there is no non-HIP fallback")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        _declare(lib)
+        ver = lib.bz_gqa_decode_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}: rebuild it")
+        _LIB = lib
+        return lib
+
+
+def status_string(code: int) -> str:
+    return load().bz_status_string(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    """Map a bz_status to the reference's error behaviour (TORCH_CHECK -> RuntimeError)."""
+    if code != 0:
+        raise RuntimeError(f"{what}: {status_string(code)} (status {code})")

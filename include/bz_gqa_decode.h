@@ -1,0 +1,127 @@
+/*
+ * bz_gqa_decode.h - C ABI of the MI355X (gfx950) GQA flash-decoding attention library
+ * (libbz_gqa_decode.so).
+ *
+ * One query token per sequence (decode step, q_len == 1) attends over a bf16 KV cache:
+ *
+ *   out[b, h, :] = sum_p softmax_p(scale * q[b, h, :] . K[b, h / G, p, :] + mask[b, p]) * V[b, h / G, p, :]
+ *
+ * over the positions p in [kv_start[b], seq_lens[b]) of row b (G = num_q_heads / num_kv_heads; q head h reads
+ * KV head h / G, the head map of repeat_kv). Positions outside that range are never read: NaN or Inf stored there
+ * cannot reach the output. Arithmetic is fp32 (online softmax in base 2, split-K partials merged by their
+ * log-sum-exp); the output is rounded to bf16 (round-to-nearest-even).
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers in an argument struct are DEVICE pointers on the current HIP device, except the struct itself.
+ *   - Strides are in ELEMENTS. The last dimension (head_dim) of every tensor is contiguous.
+ *   - The library allocates nothing and makes no host-side decision from device data, so a call can be recorded
+ *     into a HIP graph. The grid depends only on host arguments; lengths are read on the device.
+ *   - Return value: BZ_OK (0) or a negative bz_status. Nothing is launched when a check fails. No call throws.
+ *   - Calls are reentrant. Two calls that share one workspace must be ordered on one stream.
+ */
+#ifndef BZ_GQA_DECODE_H
+#define BZ_GQA_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BZ_GQA_DECODE_ABI_VERSION 1
+
+typedef enum bz_status {
+  BZ_OK = 0,
+  BZ_ERR_NULL = -1,           /* a required pointer is NULL */
+  BZ_ERR_SHAPE = -2,          /* a size is out of range or num_q_heads % num_kv_heads != 0 */
+  BZ_ERR_UNSUPPORTED = -3,    /* head_dim or GQA group size without a compiled kernel */
+  BZ_ERR_ALIGNMENT = -4,      /* K/V base pointers or strides not 16-byte aligned */
+  BZ_ERR_WORKSPACE = -5,      /* workspace NULL or smaller than bz_gqa_decode_workspace_size() */
+  BZ_ERR_MASK_DTYPE = -6,     /* mask_dtype is not one of bz_mask_dtype */
+  BZ_ERR_LAUNCH = -7,         /* hipLaunchKernelGGL / hipGetLastError reported an error */
+  BZ_ERR_DEVICE = -8,         /* hipGetDevice / hipDeviceGetAttribute failed */
+  BZ_ERR_COMBINE_MODE = -9    /* combine is not one of bz_combine_mode */
+} bz_status;
+
+typedef enum bz_mask_dtype {
+  BZ_MASK_NONE = 0,           /* no additive mask */
+  BZ_MASK_BF16 = 1,           /* bf16 additive mask (the reference's serving dtype) */
+  BZ_MASK_F32 = 2             /* fp32 additive mask */
+} bz_mask_dtype;
+
+typedef enum bz_combine_mode {
+  BZ_COMBINE_AUTO = 0,        /* library default */
+  BZ_COMBINE_LAST_BLOCK = 1,  /* the last workgroup of each (batch, kv head) merges the splits: one launch */
+  BZ_COMBINE_KERNEL = 2       /* a second kernel merges the splits: two launches */
+} bz_combine_mode;
+
+/* Arguments of bz_gqa_decode (the reference op's (q, k_cache, v_cache, seq_lens, scale) -> out). */
+typedef struct bz_gqa_decode_args {
+  /* query [batch, num_q_heads, head_dim] bf16: element (b, h, d) at q[b*q_stride_b + h*q_stride_h + d] */
+  const void* q;
+  int64_t q_stride_b, q_stride_h;
+  /* KV cache [batch, num_kv_heads, capacity, head_dim] bf16 (transformers StaticCache layer layout). K and V
+     share strides; k_cache, v_cache and all three strides must be 16-byte aligned (multiples of 8 elements). */
+  const void* k_cache;
+  const void* v_cache;
+  int64_t kv_stride_b, kv_stride_h, kv_stride_s;
+  /* [batch] int32: row b attends [kv_start[b], seq_lens[b]). kv_start may be NULL (all zeros). Values are
+     clamped on the device to 0 <= kv_start <= seq_lens <= capacity, so no access leaves the cache. */
+  const int32_t* seq_lens;
+  const int32_t* kv_start;
+  /* optional additive mask, row b at mask + b*mask_stride_b (mask_stride_b = 0 broadcasts one row), position p
+     at element p, p < capacity. A position whose mask value is <= -1e30 is excluded (the reference's threshold
+     for finfo.min); other values are added to the scaled score. */
+  const void* mask;
+  int32_t mask_dtype;         /* bz_mask_dtype */
+  int64_t mask_stride_b;
+  float scale;                /* softmax scale (head_dim ** -0.5 for the reference's layers) */
+  /* out [batch, num_q_heads, head_dim] bf16 */
+  void* out;
+  int64_t out_stride_b, out_stride_h;
+  int32_t batch, num_q_heads, num_kv_heads, head_dim, capacity;
+  /* workgroups per (batch, kv head); 0 picks bz_gqa_decode_default_splits(.., max_seq_len or capacity, ..) */
+  int32_t num_splits;
+  /* expected upper bound of seq_lens - kv_start (0 = capacity); only steers the default tiling */
+  int32_t max_seq_len;
+  int32_t combine;            /* bz_combine_mode */
+  /* caller-owned scratch of at least bz_gqa_decode_workspace_size() bytes, 256-byte aligned. It must be
+     zero-filled once before first use; the library leaves it ready for the next call. */
+  void* workspace;
+  size_t workspace_bytes;
+} bz_gqa_decode_args;
+
+/* GQA decode attention. Replaces the reference op attn_decode (flash/csrc/bb_attn.cu:416-429, pybind :463-465)
+   with the north-star signature (q, k_cache, v_cache, seq_lens, scale) -> out; kv_start carries the left-padding
+   start the reference encodes in its interval mask (backbone_graph.py:239-252). */
+int bz_gqa_decode(const bz_gqa_decode_args* args, hipStream_t stream);
+
+/* Bytes of workspace bz_gqa_decode needs for these sizes (num_splits as passed, 0 = default). Replaces the
+   caller-side sizing of the reference's scores/cmax/part/counters buffers (flash/backbone.py:27-37). */
+int bz_gqa_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 int32_t capacity, int32_t num_splits, int32_t max_seq_len, size_t* bytes);
+
+/* The split count bz_gqa_decode uses when num_splits == 0 (device CU count, sizes). No counterpart in the
+   reference, which fixes 64-position chunks at compile time (bb_attn.cu:28, :382). */
+int bz_gqa_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t capacity,
+                                 int32_t max_seq_len, int32_t* num_splits);
+
+/* Interval-mask form used by the reference's BackboneGraph: derives [kv_start, seq_end) for each row on the
+   device from an additive mask [batch or 1, capacity] (first and last position with mask > -1e30), then runs
+   bz_gqa_decode with that mask applied inside the interval. args->seq_lens / args->kv_start are ignored; args->mask
+   is required. Replaces attn_decode's mask argument (bb_attn.cu:416-418, mask scan :111-117). */
+int bz_gqa_decode_masked(const bz_gqa_decode_args* args, hipStream_t stream);
+
+/* Human-readable text of a bz_status. */
+const char* bz_status_string(int status);
+
+/* BZ_GQA_DECODE_ABI_VERSION of the loaded library. */
+int bz_gqa_decode_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BZ_GQA_DECODE_H */

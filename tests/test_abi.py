@@ -1,0 +1,138 @@
+"""The C ABI library on the CPU: it loads, exports exactly what include/*.h declares, its argument struct matches the
+C layout, and its host-side checks return the documented status codes before anything reaches the GPU.
+No call here launches a kernel (every case fails validation first)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HEADERS = sorted((REPO / "include").glob("*.h"))
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg.load()
+
+
+@pytest.fixture(scope="module")
+def K(pkg):
+    from breeze_tts_2_flash_amd import kernels
+    return kernels
+
+
+def _declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(bz_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_exports_match_header(K):
+    declared = _declared_functions()
+    assert declared == set(K.EXPORTS)
+    res = subprocess.run(["nm", "-D", "--defined-only", str(K.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = {ln.split()[-1] for ln in res.stdout.splitlines() if " T " in ln}
+    assert exported == declared
+
+
+def test_every_symbol_resolves(lib, K):
+    for name in K.EXPORTS:
+        assert getattr(lib, name) is not None
+
+
+def test_abi_version(lib, K):
+    assert lib.bz_gqa_decode_abi_version() == K.ABI_VERSION
+
+
+def test_struct_layout_matches_c(K, tmp_path):
+    fields = [f for f, _ in K.GqaDecodeArgs._fields_]
+    src = ["#include <stddef.h>", "#include <stdio.h>", '#include "bz_gqa_decode.h"', "int main(void) {",
+           '  printf("size %zu\\n", sizeof(bz_gqa_decode_args));']
+    src += [f'  printf("{f} %zu\\n", offsetof(bz_gqa_decode_args, {f}));' for f in fields]
+    src += ["  return 0;", "}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{REPO / 'include'}",
+                    str(c), "-o", str(exe)], check=True)
+    got = dict(ln.split() for ln in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                   check=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(K.GqaDecodeArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(K.GqaDecodeArgs, f).offset, f
+
+
+def test_status_strings(lib):
+    for code in range(0, -10, -1):
+        s = lib.bz_status_string(code).decode()
+        assert s and s != "unknown status"
+    assert lib.bz_status_string(-99).decode() == "unknown status"
+
+
+def _good_args(K, **over):
+    """Plausible sizes with fake (never dereferenced) device addresses; every test below breaks one check."""
+    a = K.GqaDecodeArgs()
+    a.q, a.q_stride_b, a.q_stride_h = 0x10000, 16 * 128, 128
+    a.k_cache, a.v_cache = 0x100000, 0x200000
+    a.kv_stride_b, a.kv_stride_h, a.kv_stride_s = 8 * 256 * 128, 256 * 128, 128
+    a.seq_lens = 0x30000
+    a.scale = 128 ** -0.5
+    a.out, a.out_stride_b, a.out_stride_h = 0x40000, 16 * 128, 128
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity = 2, 16, 8, 128, 256
+    a.num_splits = 4
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), -1), (dict(k_cache=None), -1), (dict(out=None), -1), (dict(seq_lens=None), -1),
+    (dict(num_kv_heads=3), -2), (dict(batch=0), -2), (dict(capacity=0), -2), (dict(kv_stride_s=64), -2),
+    (dict(head_dim=96), -3), (dict(num_q_heads=24, num_kv_heads=8), -3), (dict(num_q_heads=32, num_kv_heads=2), -3),
+    (dict(k_cache=0x100008), -4), (dict(kv_stride_s=132), -4), (dict(kv_stride_h=256 * 128 + 4), -4),
+    (dict(mask=0x50000, mask_dtype=0), -6), (dict(mask_dtype=7), -6),
+    (dict(num_splits=-1), -2), (dict(num_splits=257), -2),
+    (dict(combine=3), -9),
+    (dict(workspace=None), -5), (dict(workspace=0x60000, workspace_bytes=16), -5),
+    (dict(workspace=0x60010, workspace_bytes=1 << 30), -4),
+])
+def test_host_validation(lib, K, over, code):
+    a = _good_args(K, **over)
+    assert lib.bz_gqa_decode(ctypes.byref(a), None) == code
+    assert lib.bz_gqa_decode(None, None) == -1
+
+
+def test_masked_validation(lib, K):
+    a = _good_args(K)
+    assert lib.bz_gqa_decode_masked(ctypes.byref(a), None) == -1            # mask required
+    a = _good_args(K, mask=0x50000, mask_dtype=0)
+    assert lib.bz_gqa_decode_masked(ctypes.byref(a), None) == -6
+    a = _good_args(K, mask=0x50000, mask_dtype=1, workspace=None)
+    assert lib.bz_gqa_decode_masked(ctypes.byref(a), None) == -5
+
+
+def _ws(lib, *args):
+    n = ctypes.c_size_t(0)
+    rc = lib.bz_gqa_decode_workspace_size(*args, ctypes.byref(n))
+    return rc, n.value
+
+
+def test_workspace_size(lib):
+    def layout(B, NH, NKV, D, S):
+        a = lambda x: (x + 255) // 256 * 256  # noqa: E731
+        acc = a(B * NH * S * D * 4)
+        ml = a(acc + B * NH * S * 8)
+        cnt = a(ml + B * NKV * 4)
+        return a(cnt + 2 * B * 4)
+    for B, NH, NKV, D, cap, S in [(2, 16, 8, 128, 2048, 32), (16, 16, 8, 128, 2048, 1), (2, 8, 2, 64, 17, 3),
+                                  (1, 8, 8, 128, 4096, 256)]:
+        rc, n = _ws(lib, B, NH, NKV, D, cap, S, 0)
+        assert rc == 0 and n == layout(B, NH, NKV, D, S) and n % 256 == 0
+    assert _ws(lib, 2, 16, 8, 96, 2048, 4, 0)[0] == -3
+    assert _ws(lib, 2, 16, 8, 128, 2048, 300, 0)[0] == -2
+    assert lib.bz_gqa_decode_workspace_size(2, 16, 8, 128, 2048, 4, 0, None) == -1
