@@ -37,6 +37,7 @@ constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxSplits = 256;
 constexpr int kMaxDevices = 64;
+constexpr int kCounterStride = 64;  // ints: one 256-byte line per arrival counter (atomics to one line serialize)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kExcluded = -1e30f;  // mask values <= this exclude the position (bb_attn.cu:9-11, :115)
 
@@ -57,7 +58,7 @@ struct Params {
   int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
   float* part_acc;   // [B, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
   float2* part_ml;   // [B, NH, splits]     (m, sum_p 2^(s_p - m))
-  int* counters;     // [B, NKV]            arrivals, reset by the merging workgroup
+  int* counters;     // [B, NKV] x kCounterStride arrivals, reset by the merging workgroup
 };
 
 // ---------------------------------------------------------------------------------------------- helpers
@@ -83,6 +84,13 @@ __device__ __forceinline__ void unpack8(const uint4& w, float f[8]) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// c + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs, accumulated in fp32 (v_dot2c_f32_bf16)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
@@ -98,6 +106,27 @@ __device__ __forceinline__ float row_sum(float x) {
   x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within each 8 lanes
   if (LPR == 16) x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i within each 16 lanes
   return x;
+}
+
+// Value of lane (lane ^ OFF) for OFF in {8, 16, 32}, all on the VALU: row_ror:8 inside each 16-lane row for 8;
+// v_permlane16_swap / v_permlane32_swap for 16 / 32. A swap of x with itself leaves, in one of its two results, this
+// lane's own value and, in the other, the partner's; XOR-ing both with the own bits keeps the partner's bits
+// whichever result holds which.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float x) {
+  static_assert(OFF == 8 || OFF == 16 || OFF == 32, "lane_xor: 8, 16 or 32");
+  if constexpr (OFF == 8) {
+    return dpp<0x128>(x);
+  } else {
+    const uint32_t u = __float_as_uint(x);
+    if constexpr (OFF == 16) {
+      const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      return __uint_as_float(r[0] ^ r[1] ^ u);
+    } else {
+      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      return __uint_as_float(r[0] ^ r[1] ^ u);
+    }
+  }
 }
 
 // Clamp the row's range so that no access can leave [0, capacity).
@@ -124,48 +153,211 @@ __device__ __forceinline__ float load_mask(const void* m, int64_t off) {
   return static_cast<const float*>(m)[off];
 }
 
+// Reductions over the wave: inside 16-lane rows with DPP (quad_perm x2, half mirror, mirror), then across rows with
+// the permlane swaps. Every lane ends with the same value.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp<0xb1>(x));
+  x = fmaxf(x, dpp<0x4e>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  x = fmaxf(x, lane_xor<16>(x));
+  return fmaxf(x, lane_xor<32>(x));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row_sum<16>(x);
+  x += lane_xor<16>(x);
+  return x + lane_xor<32>(x);
+}
+
+// Split partials cross workgroups (and XCDs, each with its own L2) inside one launch, so they are written and read
+// as agent-scope relaxed atomics: on gfx950 these are sc1 accesses that write through to, and read from, the level
+// where all XCDs are coherent, with no L2 writeback or invalidate of the whole cache.
+__device__ __forceinline__ void st_agent(float* ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* ptr) {
+  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
+// Each thread owns kOut (q head, dim) outputs and issues the loads of its first kBatch split partials before the
+// split weights are known. Weights: wave g reads the (max, sum) pairs of q head g, one lane per split, and reduces
+// them with shuffles; w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s.
 template <int D, int G>
 __device__ void merge_splits(const Params& p, int b, int h, int nact) {
-  __shared__ float s_w[G][kMaxSplits];  // split maxima, then per-split weights 2^(m_s - M)
-  __shared__ float s_l[G][kMaxSplits];  // split sums
-  __shared__ float s_inv[G];            // 1 / sum_s w_s l_s
-  const int tid = threadIdx.x;
-  for (int o = tid; o < G * nact; o += kThreads) {
-    const int g = o / nact, s = o % nact;
-    const float2 ml = p.part_ml[((int64_t)b * p.NH + h * G + g) * p.splits + s];
-    s_w[g][s] = ml.x;
-    s_l[g][s] = ml.y;
+  constexpr int kBatch = 32;
+  constexpr int kOut = (G * D + kThreads - 1) / kThreads;
+  constexpr int kPerLane = kMaxSplits / kWave;
+  __shared__ float s_w[G][kMaxSplits];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int64_t row0 = (int64_t)b * p.NH + h * G;  // first q head of the group, as a [B * NH] row index
+
+  float t[kOut][kBatch];
+#pragma unroll
+  for (int k = 0; k < kOut; ++k) {
+    const int o = tid + k * kThreads;
+    if (o < G * D) {
+      const float* pa = p.part_acc + (row0 + o / D) * p.splits * D + o % D;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) t[k][u] = (u < nact) ? ld_agent(pa + (int64_t)u * D) : 0.f;
+    }
   }
-  __syncthreads();
-  if (tid < G) {
-    const int g = tid;
-    float M = -INFINITY;
-    for (int s = 0; s < nact; ++s) M = fmaxf(M, s_w[g][s]);
+
+  for (int g = wave; g < G; g += kWaves) {
+    const float* ml = reinterpret_cast<const float*>(p.part_ml + (row0 + g) * p.splits);
+    float mv[kPerLane], lv[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s = lane + kWave * j;
+      mv[j] = (s < nact) ? ld_agent(ml + 2 * s) : -INFINITY;
+      lv[j] = (s < nact) ? ld_agent(ml + 2 * s + 1) : 0.f;
+    }
+    float mloc = mv[0];
+#pragma unroll
+    for (int j = 1; j < kPerLane; ++j) mloc = fmaxf(mloc, mv[j]);
+    const float M = wave_max(mloc);
     const float mu = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f;
-    for (int s = 0; s < nact; ++s) {
-      const float w = fast_exp2(s_w[g][s] - mu);
-      s_w[g][s] = w;
-      L = fmaf(w, s_l[g][s], L);
+    float lloc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      mv[j] = fast_exp2(mv[j] - mu);
+      lloc = fmaf(mv[j], lv[j], lloc);
     }
-    s_inv[g] = L > 0.f ? 1.f / L : 0.f;
+    const float L = wave_sum(lloc);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s = lane + kWave * j;
+      if (s < nact) s_w[g][s] = mv[j] * inv;
+    }
   }
   __syncthreads();
-  for (int o = tid; o < G * D; o += kThreads) {
-    const int g = o / D, d = o % D, hq = h * G + g;
-    const float* pa = p.part_acc + ((int64_t)b * p.NH + hq) * p.splits * D + d;
+
+#pragma unroll
+  for (int k = 0; k < kOut; ++k) {
+    const int o = tid + k * kThreads;
+    if (o >= G * D) continue;
+    const int g = o / D, d = o % D;
+    const float* pa = p.part_acc + (row0 + g) * p.splits * D + d;
     float a = 0.f;
-    int s = 0;
-    for (; s + 8 <= nact; s += 8) {
-      float t[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = pa[(int64_t)(s + u) * D];
+    for (int u = 0; u < kBatch; ++u)
+      if (u < nact) a = fmaf(s_w[g][u], t[k][u], a);
+    for (int s0 = kBatch; s0 < nact; s0 += kBatch) {
+      float x[kBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) a = fmaf(s_w[g][s + u], t[u], a);
+      for (int u = 0; u < kBatch; ++u) x[u] = (s0 + u < nact) ? ld_agent(pa + (int64_t)(s0 + u) * D) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (s0 + u < nact) a = fmaf(s_w[g][s0 + u], x[u], a);
     }
-    for (; s < nact; ++s) a = fmaf(s_w[g][s], pa[(int64_t)s * D], a);
-    p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(a * s_inv[g]);
+    p.out[(int64_t)b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
+  }
+}
+
+// One tile of KV rows held in VGPRs: position pos0 + ROWS * i for i < PPT (pos0 = tile start + this lane's row).
+template <int PPT>
+struct Tile {
+  uint4 k[PPT], v[PPT];
+  float m[PPT];
+};
+
+// Issue every K and V load of a tile (and its mask values) before any arithmetic. Positions >= hi are not read.
+template <int ROWS, int PPT, int MK>
+__device__ __forceinline__ void load_tile(Tile<PPT>& t, const uint16_t* kb, const uint16_t* vb, int64_t ss,
+                                          const void* mask, int64_t mrow, int pos0, int hi) {
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int pos = pos0 + ROWS * i;
+    if (pos < hi) {
+      t.k[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)pos * ss);
+      t.v[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)pos * ss);
+    } else {
+      t.k[i] = make_uint4(0, 0, 0, 0);
+      t.v[i] = make_uint4(0, 0, 0, 0);
+    }
+    if (MK != BZ_MASK_NONE) t.m[i] = (pos < hi) ? load_mask<MK>(mask, mrow + pos) : 0.f;
+  }
+}
+
+// Fold one tile into this row's running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP
+// row sum, scaled by scale * log2(e); online softmax in base 2; then P.V in fp32 on the unpacked V registers.
+// A slot whose row lies past hi is skipped (the condition is uniform over the row's lanes, so the DPP sum, which
+// reads only lanes of the same row, never sees a skipped lane).
+template <int LPR, int ROWS, int G, int PPT, int MK>
+__device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G], float scale_log2, float (&m)[G],
+                                             float (&l)[G], float (&acc)[G][8], int pos0, int hi) {
+  float s[G][PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[g][i] = -INFINITY;
+    const int pos = pos0 + ROWS * i;
+    if (pos < hi) {
+      bool inc = true;
+      if (MK != BZ_MASK_NONE) {
+        inc = t.m[i] > kExcluded;
+        // an excluded position must not touch the accumulator even through 0 * V (V may hold NaN there)
+        if (!inc) t.v[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = dot2_bf16(qp[g].x, t.k[i].x, 0.f);
+        d = dot2_bf16(qp[g].y, t.k[i].y, d);
+        d = dot2_bf16(qp[g].z, t.k[i].z, d);
+        d = dot2_bf16(qp[g].w, t.k[i].w, d);
+        d = row_sum<LPR>(d) * scale_log2;
+        if (MK != BZ_MASK_NONE) d = fmaf(t.m[i], kLog2e, d);
+        if (inc) s[g][i] = d;
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mt = s[g][0];
+#pragma unroll
+    for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
+    const float mn = fmaxf(m[g], mt);
+    const float mu = (mn == -INFINITY) ? 0.f : mn;
+    const float alpha = fast_exp2(m[g] - mu);
+    l[g] *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      s[g][i] = fast_exp2(s[g][i] - mu);
+      l[g] += s[g][i];
+    }
+    m[g] = mn;
+  }
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    if (pos0 + ROWS * i < hi) {
+      float vf[8];
+      unpack8(t.v[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
+    }
+  }
+}
+
+// Merge this lane's (m, l, acc) with lane (lane ^ OFF)'s, which holds the same dims of another KV row, by the
+// log-sum-exp rule. Both lanes end with the same state.
+template <int OFF, int G>
+__device__ __forceinline__ void merge_rows(float (&m)[G], float (&l)[G], float (&acc)[G][8]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mo = lane_xor<OFF>(m[g]);
+    const float lo = lane_xor<OFF>(l[g]);
+    const float mn = fmaxf(m[g], mo);
+    const float mu = (mn == -INFINITY) ? 0.f : mn;
+    const float a = fast_exp2(m[g] - mu), bo = fast_exp2(mo - mu);
+    l[g] = l[g] * a + lo * bo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = acc[g][j] * a + lane_xor<OFF>(acc[g][j]) * bo;
+    m[g] = mn;
   }
 }
 
@@ -182,6 +374,15 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
 
+  // q of the G heads of this group, this lane's 8 dims: issued first, since it does not depend on the row's length
+  uint16_t qh[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint16_t* qsrc = p.q + (int64_t)b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + 8 * c;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qh[g][j] = qsrc[j];
+  }
+
   int start, end;
   row_range(p, b, start, end);
   const int len = end - start;
@@ -191,13 +392,26 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
   const int lo = start + split * chunk;
   const int hi = min(lo + chunk, end);
 
-  // q of the G heads of this group, this lane's 8 dims, scaled by scale * log2(e)
-  float qf[G][8];
+  const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + 8 * c;
+  const uint16_t* kb = p.k + head_off;
+  const uint16_t* vb = p.v + head_off;
+  const int64_t mrow = (int64_t)b * p.m_sb;
+
+  // The first tile's K/V loads (and, for PPT <= 4, the second's) go out before q is converted, so no wave waits on
+  // q before streaming. Tiles A and B ping-pong without register copies: while one is consumed the other's loads
+  // are in flight. Loads of positions >= hi are skipped, so a one-tile chunk issues no extra traffic.
+  constexpr bool kPingPong = PPT <= 4;
+  Tile<PPT> ta, tb;
+  load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, lo + r, hi);
+  if (kPingPong) load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, lo + TP + r, hi);
+
+  uint4 qp[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + 8 * c;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qf[g][j] = bf16_to_f32(qp[j]) * p.scale_log2;
+    qp[g].x = qh[g][0] | ((uint32_t)qh[g][1] << 16);
+    qp[g].y = qh[g][2] | ((uint32_t)qh[g][3] << 16);
+    qp[g].z = qh[g][4] | ((uint32_t)qh[g][5] << 16);
+    qp[g].w = qh[g][6] | ((uint32_t)qh[g][7] << 16);
   }
 
   float m[G], l[G], acc[G][8];
@@ -209,96 +423,25 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
   }
 
-  const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + 8 * c;
-  const uint16_t* kb = p.k + head_off;
-  const uint16_t* vb = p.v + head_off;
-  const int64_t mrow = (int64_t)b * p.m_sb;
-
-  for (int t0 = lo; t0 < hi; t0 += TP) {
-    uint4 kr[PPT], vr[PPT];
-    float mv[PPT];
-    // issue every K and V load of the tile before any arithmetic
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int pos = t0 + r + ROWS * i;
-      if (pos < hi) {
-        kr[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)pos * p.kv_ss);
-        vr[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)pos * p.kv_ss);
-      } else {
-        kr[i] = make_uint4(0, 0, 0, 0);
-        vr[i] = make_uint4(0, 0, 0, 0);
-      }
-      if (MK != BZ_MASK_NONE) mv[i] = (pos < hi) ? load_mask<MK>(p.mask, mrow + pos) : 0.f;
+  if (kPingPong) {
+    for (int t0 = lo; t0 < hi; t0 += 2 * TP) {
+      consume_tile<LPR, ROWS, G, PPT, MK>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi);
+      if (t0 + TP >= hi) break;
+      load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + 2 * TP + r, hi);
+      consume_tile<LPR, ROWS, G, PPT, MK>(tb, qp, p.scale_log2, m, l, acc, t0 + TP + r, hi);
+      load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, t0 + 3 * TP + r, hi);
     }
-
-    float s[G][PPT];
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int pos = t0 + r + ROWS * i;
-      float kf[8];
-      unpack8(kr[i], kf);
-      bool inc = pos < hi;
-      if (MK != BZ_MASK_NONE) {
-        inc = inc && (mv[i] > kExcluded);
-        // an excluded position must not touch the accumulator even through 0 * V (V may hold NaN there)
-        if (!inc) vr[i] = make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) d = fmaf(qf[g][j], kf[j], d);
-        d = row_sum<LPR>(d);
-        if (MK != BZ_MASK_NONE) d = fmaf(mv[i], kLog2e, d);
-        s[g][i] = inc ? d : -INFINITY;
-      }
-    }
-
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mt = s[g][0];
-#pragma unroll
-      for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
-      const float mn = fmaxf(m[g], mt);
-      const float mu = (mn == -INFINITY) ? 0.f : mn;
-      const float alpha = fast_exp2(m[g] - mu);
-      l[g] *= alpha;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
-#pragma unroll
-      for (int i = 0; i < PPT; ++i) {
-        s[g][i] = fast_exp2(s[g][i] - mu);
-        l[g] += s[g][i];
-      }
-      m[g] = mn;
-    }
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      float vf[8];
-      unpack8(vr[i], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
+  } else {
+    for (int t0 = lo; t0 < hi; t0 += TP) {
+      consume_tile<LPR, ROWS, G, PPT, MK>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi);
+      if (t0 + TP < hi) load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + TP + r, hi);
     }
   }
 
   // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims)
-#pragma unroll
-  for (int off = LPR; off < kWave; off <<= 1) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mo = __shfl_xor(m[g], off);
-      const float lo2 = __shfl_xor(l[g], off);
-      const float mn = fmaxf(m[g], mo);
-      const float mu = (mn == -INFINITY) ? 0.f : mn;
-      const float a = fast_exp2(m[g] - mu), bo = fast_exp2(mo - mu);
-      l[g] = l[g] * a + lo2 * bo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] = acc[g][j] * a + __shfl_xor(acc[g][j], off) * bo;
-      m[g] = mn;
-    }
-  }
+  if (LPR == 8) merge_rows<8, G>(m, l, acc);
+  merge_rows<16, G>(m, l, acc);
+  merge_rows<32, G>(m, l, acc);
 
   // merge the 4 waves through LDS
   __shared__ float s_acc[kWaves][G][D];
@@ -335,24 +478,30 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
       p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(L > 0.f ? A / L : 0.f);
     } else {
       const int64_t ps = ((int64_t)b * p.NH + hq) * p.splits + split;
-      p.part_acc[ps * D + d] = A;
-      if (d == 0) p.part_ml[ps] = make_float2(M, L);
+      st_agent(p.part_acc + ps * D + d, A);
+      if (d == 0) {
+        st_agent(reinterpret_cast<float*>(p.part_ml + ps), M);
+        st_agent(reinterpret_cast<float*>(p.part_ml + ps) + 1, L);
+      }
     }
   }
   if (nact == 1 || !p.combine_last) return;
 
-  // last-arriving workgroup of this (b, kv head) merges the splits
+  // Last-arriving workgroup of this (b, kv head) merges the splits. Each wave waits until its agent-scope partial
+  // stores have completed (s_waitcnt vmcnt(0); gfx9 encoding with expcnt/lgkmcnt left open), the barrier collects
+  // the four waves, and thread 0 counts the workgroup in with one agent-scope RMW. The workgroup that brings the
+  // count to nact reads the partials with agent-scope loads; it resets the counter for the next call.
   __shared__ int s_last;
-  __threadfence();  // release this workgroup's partials at device scope
+  __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
   if (tid == 0) {
-    const int prev = atomicAdd(&p.counters[b * p.NKV + h], 1);
+    int* cnt = p.counters + (b * p.NKV + h) * kCounterStride;
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == nact - 1);
+    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();  // acquire the other workgroups' partials
-  if (tid == 0) p.counters[b * p.NKV + h] = 0;
   merge_splits<D, G>(p, b, h, nact);
 }
 
@@ -457,15 +606,16 @@ bool supported_dim(int D) { return D == 64 || D == 128; }
 // Smallest chunk a split gets: 16 KB of K+V (32 positions at head_dim 128, 64 at head_dim 64).
 int min_chunk_for(int D) { return (16 * 1024) / (4 * D); }
 
-// Positions per thread per tile: the smallest power of two whose tile covers the expected chunk, capped so that
-// the K/V registers (2 * PPT * 4 VGPRs) plus q and the accumulators (16 * G VGPRs) stay in budget.
+// Positions per thread per tile. Two tiles (A, B) are in flight from the start, so the expected chunk is covered by
+// at least two tiles when possible: the first tile's arithmetic then overlaps the second tile's arrival. PPT is the
+// smallest power of two with 2 * rows * PPT >= chunk, capped at 4 (ping-pong registers: 2 tiles * 2 * PPT * 4 VGPRs)
+// and lower for wide GQA groups (accumulators take 8 * G VGPRs).
 int ppt_for(int D, int G, int chunk) {
   const int rows = kThreads / (D / 8);
-  int cap = 8;
+  int cap = 4;
   if (G >= 8) cap = 2;
-  else if (G >= 4) cap = 4;
   int ppt = 1;
-  while (ppt < cap && rows * ppt < chunk) ppt <<= 1;
+  while (ppt < cap && 2 * rows * ppt < chunk) ppt <<= 1;
   return ppt;
 }
 
@@ -493,11 +643,16 @@ int effective_len(int capacity, int max_seq_len) {
   return (max_seq_len > 0 && max_seq_len < capacity) ? max_seq_len : capacity;
 }
 
+// Split count: enough workgroups to give every CU one (cus / units splits), and no chunk longer than kMaxChunk
+// positions even in the longest row (a chunk streams through one workgroup two tiles at a time, so its latency grows
+// with its length), but no split shorter than min_chunk positions.
 int default_splits_for(int units, int D, int len, int cus) {
+  constexpr int kMaxChunk = 256;
   const int min_chunk = min_chunk_for(D);
   const int useful = len > 0 ? (len + min_chunk - 1) / min_chunk : 1;
-  const int target = 2 * cus;  // two workgroups per CU
-  int s = (target + units - 1) / units;
+  int s = (cus + units - 1) / units;
+  const int by_len = (len + kMaxChunk - 1) / kMaxChunk;
+  if (s < by_len) s = by_len;
   if (s > useful) s = useful;
   if (s > kMaxSplits) s = kMaxSplits;
   return s < 1 ? 1 : s;
@@ -514,7 +669,7 @@ WsLayout ws_layout(int B, int NH, int NKV, int D, int splits) {
   w.acc = 0;
   w.ml = align256(w.acc + (size_t)B * NH * splits * D * sizeof(float));
   w.counters = align256(w.ml + (size_t)B * NH * splits * sizeof(float2));
-  w.ranges = align256(w.counters + (size_t)B * NKV * sizeof(int));
+  w.ranges = align256(w.counters + (size_t)B * NKV * kCounterStride * sizeof(int));
   w.total = align256(w.ranges + (size_t)2 * B * sizeof(int32_t));
   return w;
 }
