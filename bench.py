@@ -36,10 +36,14 @@ def parse_args():
     p.add_argument("--combine", default="auto", choices=["auto", "last_block", "kernel"])
     p.add_argument("--splits", type=int, default=0, help="0 = library default")
     p.add_argument("--eager", action="store_true", help="launch each call from Python instead of a HIP graph")
+    p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4],
+                   help="headline workload (BASELINE config; 2 is the metric's serving shape)")
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--traffic-bytes", type=float, default=None,
-                   help="HBM bytes per call of the split kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE runs")
+                   help="HBM bytes per call (overrides the value read from profiles/)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                   help="only run device-to-device copies of BYTES (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -160,6 +164,43 @@ def cpu_baseline(w, calls=200, warmup=20):
     return statistics.median(ts) / 1000.0, torch.get_num_threads(), len(ts)
 
 
+WORKLOADS = {
+    1: "config 1: reference CPU step, B2, 16q/8kv, D128, K/V 256, seq_lens 256",
+    2: "config 2: backbone decode, B2, 16q/8kv, D128, capacity 2048, seq_lens 1024",
+    3: "config 3: long split-K, B2, 16q/8kv, D128, capacity 4096, seq_lens 4096, 1% of K x8",
+    4: "config 4: ragged server batch, B16 (8 CFG pairs), 16q/8kv, D128, capacity 2048, lengths U[128, 2048]",
+}
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "gqa_split_kernel_config2_traffic.txt")
+
+
+def traffic_from_profile():
+    """HBM bytes per call recorded by the rocprofv3 counter runs summarised in profiles/ (None if absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(nbytes, steps):
+    """Plain device-to-device copies of nbytes: each dispatch reads and writes exactly nbytes, the reference for
+    scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": steps}), flush=True)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -177,43 +218,50 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, args.steps)
+        return
     pkg.load()
 
-    w2 = workloads.make(2)
-    splits2 = args.splits or pkg.default_splits(2, 8, 128, w2.capacity, 0)
-    print(f"[bench] config 2 cold, {args.steps} calls, splits={splits2}, combine={args.combine}", file=sys.stderr,
+    cfg = args.config
+    w2 = workloads.make(cfg)
+    splits2 = args.splits or pkg.default_splits(w2.batch, w2.num_kv_heads, w2.head_dim, w2.capacity, 0)
+    print(f"[bench] config {cfg} cold, {args.steps} calls, splits={splits2}, combine={args.combine}", file=sys.stderr,
           flush=True)
     us, nbytes, nsets = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
                                    cold=True)
     gbs = nbytes / us / 1e3
-    print(f"[bench] config 2 cold: {us:.3f} us/call, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+    print(f"[bench] config {cfg} cold: {us:.3f} us/call, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "config 2: backbone decode, B2, 16q/8kv, D128, capacity 2048, seq_lens 1024",
+        "config": {"workload": WORKLOADS[cfg],
                    "us_per_call": round(us, 3), "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                    "storage": "bf16", "splits": splits2, "combine": args.combine,
                    "timing": "eager launches" if args.eager else "HIP graph replay, HIP events on the launch stream",
                    "cache": f"cold: {nsets} rotating K/V sets", "algorithmic_bytes_per_call": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": args.traffic_bytes},
+                     "traffic": args.traffic_bytes if args.traffic_bytes is not None else
+                     (traffic_from_profile() if cfg == 2 else None)},
     }
     extra = {}
     if not args.no_extra:
         us_w, _, _ = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
                                 cold=False)
-        extra["config2_warm"] = {"us_per_call": round(us_w, 3), "GB/s": round(nbytes / us_w / 1e3, 1)}
-        print(f"[bench] config 2 warm: {us_w:.3f} us/call", file=sys.stderr, flush=True)
-        for cfg in (3, 4):
-            w = workloads.make(cfg)
+        extra[f"config{cfg}_warm"] = {"us_per_call": round(us_w, 3), "GB/s": round(nbytes / us_w / 1e3, 1)}
+        print(f"[bench] config {cfg} warm: {us_w:.3f} us/call", file=sys.stderr, flush=True)
+        for xc in (2, 3, 4):
+            if xc == cfg:
+                continue
+            w = workloads.make(xc)
             us_c, nb, ns = time_calls(pkg, w, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
                                       cold=True)
-            extra[f"config{cfg}_cold"] = {
-                "workload": workloads.NAMES[cfg], "us_per_call": round(us_c, 3), "GB/s": round(nb / us_c / 1e3, 1),
+            extra[f"config{xc}_cold"] = {
+                "workload": workloads.NAMES[xc], "us_per_call": round(us_c, 3), "GB/s": round(nb / us_c / 1e3, 1),
                 "pct_of_peak_hbm": round(100.0 * nb / us_c / 1e3 / PEAK_HBM_GBS, 1), "bytes": nb, "sets": ns}
-            print(f"[bench] config {cfg} cold: {us_c:.3f} us/call, {nb / us_c / 1e3:.1f} GB/s", file=sys.stderr,
+            print(f"[bench] config {xc} cold: {us_c:.3f} us/call, {nb / us_c / 1e3:.1f} GB/s", file=sys.stderr,
                   flush=True)
             del w
         us_f, fb = time_depth_frame(pkg, dev, args.steps, args.warmup)
@@ -225,8 +273,9 @@ def main():
         us_cpu, cores, n = cpu_baseline(w2)
         line["cpu_baseline"] = {"value": round(nbytes / us_cpu / 1e3, 3), "unit": "GB/s", "cores": cores,
                                 "kind": "port", "us_per_call": round(us_cpu, 1),
-                                "sample": f"config 2 inputs, eager bf16 chain over capacity 2048 with the interval "
-                                          f"mask, median of {n} calls after 20 warmups"}
+                                "sample": f"config {cfg} inputs, the reference's eager bf16 chain over the full "
+                                          f"{w2.capacity}-slot cache with the interval mask, median of {n} calls "
+                                          f"after 20 warmups"}
         print(f"[bench] cpu baseline: {us_cpu:.1f} us/call on {cores} threads", file=sys.stderr, flush=True)
     print(json.dumps(line), flush=True)
 

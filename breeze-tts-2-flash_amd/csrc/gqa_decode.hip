@@ -180,38 +180,44 @@ __device__ __forceinline__ float ld_agent(const float* ptr) {
 }
 
 // Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
-// Each thread owns kOut (q head, dim) outputs and issues the loads of its first kBatch split partials before the
-// split weights are known. Weights: wave g reads the (max, sum) pairs of q head g, one lane per split, and reduces
-// them with shuffles; w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s.
-template <int D, int G>
+// Every load the merge needs is issued before anything waits: each thread's first kBatch split partials for its kOut
+// (q head, dim) outputs, and the (max, sum) pairs of q head `wave` (one lane per split). Split weights
+// w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s are reduced over the wave with DPP and lane swaps and stored to LDS
+// zero-padded, so the weighted sum over the first kBatch splits needs no per-split condition.
+template <int D, int G, int NT>
 __device__ void merge_splits(const Params& p, int b, int h, int nact) {
   constexpr int kBatch = 32;
-  constexpr int kOut = (G * D + kThreads - 1) / kThreads;
+  constexpr int NW = NT / kWave;
+  constexpr int kOut = (G * D + NT - 1) / NT;
   constexpr int kPerLane = kMaxSplits / kWave;
-  __shared__ float s_w[G][kMaxSplits];
+  __shared__ __align__(16) float s_w[G][kMaxSplits];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int64_t row0 = (int64_t)b * p.NH + h * G;  // first q head of the group, as a [B * NH] row index
 
   float t[kOut][kBatch];
 #pragma unroll
   for (int k = 0; k < kOut; ++k) {
-    const int o = tid + k * kThreads;
+    const int o = tid + k * NT;
     if (o < G * D) {
       const float* pa = p.part_acc + (row0 + o / D) * p.splits * D + o % D;
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) t[k][u] = (u < nact) ? ld_agent(pa + (int64_t)u * D) : 0.f;
     }
   }
-
-  for (int g = wave; g < G; g += kWaves) {
+  float mv[kPerLane], lv[kPerLane];
+  auto load_ml = [&](int g) {
     const float* ml = reinterpret_cast<const float*>(p.part_ml + (row0 + g) * p.splits);
-    float mv[kPerLane], lv[kPerLane];
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
       const int s = lane + kWave * j;
       mv[j] = (s < nact) ? ld_agent(ml + 2 * s) : -INFINITY;
       lv[j] = (s < nact) ? ld_agent(ml + 2 * s + 1) : 0.f;
     }
+  };
+  if (wave < G) load_ml(wave);
+
+  for (int g = wave; g < G; g += NW) {
+    if (g != wave) load_ml(g);
     float mloc = mv[0];
 #pragma unroll
     for (int j = 1; j < kPerLane; ++j) mloc = fmaxf(mloc, mv[j]);
@@ -220,36 +226,31 @@ __device__ void merge_splits(const Params& p, int b, int h, int nact) {
     float lloc = 0.f;
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
-      mv[j] = fast_exp2(mv[j] - mu);
+      mv[j] = fast_exp2(mv[j] - mu);  // 0 for the padding (-inf)
       lloc = fmaf(mv[j], lv[j], lloc);
     }
     const float L = wave_sum(lloc);
     const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-      const int s = lane + kWave * j;
-      if (s < nact) s_w[g][s] = mv[j] * inv;
-    }
+    for (int j = 0; j < kPerLane; ++j) s_w[g][lane + kWave * j] = mv[j] * inv;
   }
   __syncthreads();
 
 #pragma unroll
   for (int k = 0; k < kOut; ++k) {
-    const int o = tid + k * kThreads;
+    const int o = tid + k * NT;
     if (o >= G * D) continue;
     const int g = o / D, d = o % D;
     const float* pa = p.part_acc + (row0 + g) * p.splits * D + d;
     float a = 0.f;
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (u < nact) a = fmaf(s_w[g][u], t[k][u], a);
+    for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][u], t[k][u], a);
     for (int s0 = kBatch; s0 < nact; s0 += kBatch) {
       float x[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) x[u] = (s0 + u < nact) ? ld_agent(pa + (int64_t)(s0 + u) * D) : 0.f;
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        if (s0 + u < nact) a = fmaf(s_w[g][s0 + u], x[u], a);
+      for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][s0 + u], x[u], a);
     }
     p.out[(int64_t)b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
   }
@@ -280,8 +281,9 @@ __device__ __forceinline__ void load_tile(Tile<PPT>& t, const uint16_t* kb, cons
   }
 }
 
-// Fold one tile into this row's running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP
-// row sum, scaled by scale * log2(e); online softmax in base 2; then P.V in fp32 on the unpacked V registers.
+// Fold one tile into the running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP row sum,
+// scaled by scale * log2(e); online softmax in base 2 with one max per wave (m is wave-uniform, l and acc per row);
+// then P.V in fp32 on the unpacked V registers.
 // A slot whose row lies past hi is skipped (the condition is uniform over the row's lanes, so the DPP sum, which
 // reads only lanes of the same row, never sees a skipped lane).
 template <int LPR, int ROWS, int G, int PPT, int MK>
@@ -317,6 +319,10 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
     float mt = s[g][0];
 #pragma unroll
     for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
+    // one running max per wave: the rows of a wave can then be merged by plain sums
+    if (LPR == 8) mt = fmaxf(mt, lane_xor<8>(mt));
+    mt = fmaxf(mt, lane_xor<16>(mt));
+    mt = fmaxf(mt, lane_xor<32>(mt));
     const float mn = fmaxf(m[g], mt);
     const float mu = (mn == -INFINITY) ? 0.f : mn;
     const float alpha = fast_exp2(m[g] - mu);
@@ -343,30 +349,25 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
   }
 }
 
-// Merge this lane's (m, l, acc) with lane (lane ^ OFF)'s, which holds the same dims of another KV row, by the
-// log-sum-exp rule. Both lanes end with the same state.
+// Add lane (lane ^ OFF)'s (l, acc), which covers the same dims for other KV rows under the same wave-uniform max.
+// Both lanes end with the same sums.
 template <int OFF, int G>
-__device__ __forceinline__ void merge_rows(float (&m)[G], float (&l)[G], float (&acc)[G][8]) {
+__device__ __forceinline__ void sum_rows(float (&l)[G], float (&acc)[G][8]) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float mo = lane_xor<OFF>(m[g]);
-    const float lo = lane_xor<OFF>(l[g]);
-    const float mn = fmaxf(m[g], mo);
-    const float mu = (mn == -INFINITY) ? 0.f : mn;
-    const float a = fast_exp2(m[g] - mu), bo = fast_exp2(mo - mu);
-    l[g] = l[g] * a + lo * bo;
+    l[g] += lane_xor<OFF>(l[g]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] = acc[g][j] * a + lane_xor<OFF>(acc[g][j]) * bo;
-    m[g] = mn;
+    for (int j = 0; j < 8; ++j) acc[g][j] += lane_xor<OFF>(acc[g][j]);
   }
 }
 
 // ---------------------------------------------------------------------------------------------- kernels
 
-template <int D, int G, int PPT, int MK>
-__global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
+template <int D, int G, int PPT, int MK, int NT>
+__global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
+  constexpr int NW = NT / kWave;        // waves per workgroup
   constexpr int LPR = D / 8;            // lanes per KV row, 16 B (8 bf16) each
-  constexpr int ROWS = kThreads / LPR;  // KV rows per load instruction across the workgroup
+  constexpr int ROWS = NT / LPR;        // KV rows per load instruction across the workgroup
   constexpr int TP = ROWS * PPT;        // positions per tile
   constexpr int RPW = kWave / LPR;      // rows per wave
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
@@ -439,13 +440,13 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
   }
 
   // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims)
-  if (LPR == 8) merge_rows<8, G>(m, l, acc);
-  merge_rows<16, G>(m, l, acc);
-  merge_rows<32, G>(m, l, acc);
+  if (LPR == 8) sum_rows<8, G>(l, acc);
+  sum_rows<16, G>(l, acc);
+  sum_rows<32, G>(l, acc);
 
-  // merge the 4 waves through LDS
-  __shared__ float s_acc[kWaves][G][D];
-  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
+  // merge the NW waves through LDS
+  __shared__ float s_acc[NW][G][D];
+  __shared__ float s_m[NW][G], s_l[NW][G];
   const int w = tid / kWave, lane = tid % kWave;
   if (lane < LPR) {
 #pragma unroll
@@ -461,15 +462,15 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
   __syncthreads();
   (void)RPW;
 
-  for (int o = tid; o < G * D; o += kThreads) {
+  for (int o = tid; o < G * D; o += NT) {
     const int g = o / D, d = o % D, hq = h * G + g;
     float M = s_m[0][g];
 #pragma unroll
-    for (int u = 1; u < kWaves; ++u) M = fmaxf(M, s_m[u][g]);
+    for (int u = 1; u < NW; ++u) M = fmaxf(M, s_m[u][g]);
     const float mu = (M == -INFINITY) ? 0.f : M;
     float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int u = 0; u < kWaves; ++u) {
+    for (int u = 0; u < NW; ++u) {
       const float e = fast_exp2(s_m[u][g] - mu);
       L = fmaf(e, s_l[u][g], L);
       A = fmaf(e, s_acc[u][g][d], A);
@@ -489,7 +490,7 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
 
   // Last-arriving workgroup of this (b, kv head) merges the splits. Each wave waits until its agent-scope partial
   // stores have completed (s_waitcnt vmcnt(0); gfx9 encoding with expcnt/lgkmcnt left open), the barrier collects
-  // the four waves, and thread 0 counts the workgroup in with one agent-scope RMW. The workgroup that brings the
+  // the waves, and thread 0 counts the workgroup in with one agent-scope RMW. The workgroup that brings the
   // count to nact reads the partials with agent-scope loads; it resets the counter for the next call.
   __shared__ int s_last;
   __builtin_amdgcn_s_waitcnt(0x0f70);
@@ -502,7 +503,7 @@ __global__ void __launch_bounds__(kThreads) gqa_split_kernel(const Params p) {
   }
   __syncthreads();
   if (!s_last) return;
-  merge_splits<D, G>(p, b, h, nact);
+  merge_splits<D, G, NT>(p, b, h, nact);
 }
 
 // Second-launch merge: one workgroup per (kv head, row).
@@ -514,7 +515,7 @@ __global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
   const int len = end - start;
   const int nact = split_count(len, split_chunk(len, p.splits, p.min_chunk));
   if (nact == 1) return;  // the split kernel wrote the output
-  merge_splits<D, G>(p, b, h, nact);
+  merge_splits<D, G, kThreads>(p, b, h, nact);
 }
 
 // Interval of the additive mask row: first and last position with value > -1e30.
@@ -555,39 +556,38 @@ __global__ void __launch_bounds__(kThreads) mask_range_kernel(const void* mask, 
 
 using SplitFn = void (*)(const Params);
 
-template <int D, int G, int MK>
+template <int D, int G, int MK, int NT>
 SplitFn pick_ppt(int ppt) {
   switch (ppt) {
-    case 1: return gqa_split_kernel<D, G, 1, MK>;
-    case 2: return gqa_split_kernel<D, G, 2, MK>;
-    case 4: return gqa_split_kernel<D, G, 4, MK>;
-    default: return gqa_split_kernel<D, G, 8, MK>;
+    case 1: return gqa_split_kernel<D, G, 1, MK, NT>;
+    case 2: return gqa_split_kernel<D, G, 2, MK, NT>;
+    default: return gqa_split_kernel<D, G, 4, MK, NT>;
   }
 }
 
-template <int D, int G>
+template <int D, int G, int NT>
 SplitFn pick_mask(int mk, int ppt) {
   switch (mk) {
-    case BZ_MASK_BF16: return pick_ppt<D, G, BZ_MASK_BF16>(ppt);
-    case BZ_MASK_F32: return pick_ppt<D, G, BZ_MASK_F32>(ppt);
-    default: return pick_ppt<D, G, BZ_MASK_NONE>(ppt);
+    case BZ_MASK_BF16: return pick_ppt<D, G, BZ_MASK_BF16, NT>(ppt);
+    case BZ_MASK_F32: return pick_ppt<D, G, BZ_MASK_F32, NT>(ppt);
+    default: return pick_ppt<D, G, BZ_MASK_NONE, NT>(ppt);
   }
 }
 
-template <int D>
+template <int D, int NT>
 SplitFn pick_group(int G, int mk, int ppt) {
   switch (G) {
-    case 1: return pick_mask<D, 1>(mk, ppt);
-    case 2: return pick_mask<D, 2>(mk, ppt);
-    case 4: return pick_mask<D, 4>(mk, ppt);
-    case 8: return pick_mask<D, 8>(mk, ppt);
+    case 1: return pick_mask<D, 1, NT>(mk, ppt);
+    case 2: return pick_mask<D, 2, NT>(mk, ppt);
+    case 4: return pick_mask<D, 4, NT>(mk, ppt);
+    case 8: return pick_mask<D, 8, NT>(mk, ppt);
     default: return nullptr;
   }
 }
 
-SplitFn pick_split(int D, int G, int mk, int ppt) {
-  if (D == 128) return pick_group<128>(G, mk, ppt);
-  if (D == 64) return pick_group<64>(G, mk, ppt);
+SplitFn pick_split(int D, int G, int mk, int ppt, int nt) {
+  if (D == 128) return nt == 512 ? pick_group<128, 512>(G, mk, ppt) : pick_group<128, 256>(G, mk, ppt);
+  if (D == 64) return nt == 512 ? pick_group<64, 512>(G, mk, ppt) : pick_group<64, 256>(G, mk, ppt);
   return nullptr;
 }
 
@@ -610,13 +610,21 @@ int min_chunk_for(int D) { return (16 * 1024) / (4 * D); }
 // at least two tiles when possible: the first tile's arithmetic then overlaps the second tile's arrival. PPT is the
 // smallest power of two with 2 * rows * PPT >= chunk, capped at 4 (ping-pong registers: 2 tiles * 2 * PPT * 4 VGPRs)
 // and lower for wide GQA groups (accumulators take 8 * G VGPRs).
-int ppt_for(int D, int G, int chunk) {
-  const int rows = kThreads / (D / 8);
+int ppt_for(int D, int G, int chunk, int nt) {
+  const int rows = nt / (D / 8);
   int cap = 4;
   if (G >= 8) cap = 2;
   int ppt = 1;
   while (ppt < cap && 2 * rows * ppt < chunk) ppt <<= 1;
   return ppt;
+}
+
+// Threads per split workgroup: 512 (8 waves, two per SIMD, so one wave's VALU latency hides behind the other's)
+// when the grid has at most one workgroup per CU and the chunk fills a 512-thread tile; 256 otherwise (more
+// workgroups already give each SIMD several waves), and for G = 8, whose accumulators need the registers.
+int threads_for(int D, int G, int chunk, int64_t workgroups, int cus) {
+  if (G >= 8 || workgroups > cus) return 256;
+  return chunk >= 512 / (D / 8) ? 512 : 256;
 }
 
 std::atomic<int> g_cu_count[kMaxDevices];
@@ -712,8 +720,12 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   const int len = effective_len(cap, a->max_seq_len);
   int chunk = (len + splits - 1) / splits;
   if (chunk < min_chunk) chunk = min_chunk;
-  const int ppt = ppt_for(D, G, chunk);
-  SplitFn split_fn = pick_split(D, G, mask_kind, ppt);
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc != BZ_OK) return rc;
+  const int nt = threads_for(D, G, chunk, (int64_t)splits * NKV * B, cus);
+  const int ppt = ppt_for(D, G, chunk, nt);
+  SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt);
   SplitFn comb_fn = pick_combine(D, G);
   if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
 
@@ -747,7 +759,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   p.part_ml = reinterpret_cast<float2*>(wsb + ws.ml);
   p.counters = reinterpret_cast<int*>(wsb + ws.counters);
 
-  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, B), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, B), dim3(nt), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
   if (two_kernels && splits > 1) {
     hipLaunchKernelGGL(comb_fn, dim3(NKV, B), dim3(kThreads), 0, stream, p);
