@@ -340,3 +340,25 @@ def test_argument_errors(device):
     with pytest.raises(RuntimeError, match="dbg"):
         attn_decode(g.q[:, :, None], g.k, g.v, torch.zeros(2, 1, 1, 64, device=device), 0.1, None, None, None, None,
                     torch.empty(2, 1, 16, 128, dtype=torch.bfloat16, device=device), dbg=torch.empty(1))
+
+
+# ---------------------------------------------------------------------------------------------- golden fixtures
+
+def test_golden_fixtures(device):
+    """The committed fixtures (tests/golden/decode_attention.npz), through gqa_decode and, for the masked case, also
+    through the interval-mask entry point."""
+    from tests.golden.make_golden import load
+
+    for name, c in sorted(load().items()):
+        t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)  # noqa: E731
+        q, k, v = t(c["q"]), t(c["k"]), t(c["v"])
+        lens = torch.from_numpy(c["lens"]).to(device)
+        starts = torch.from_numpy(c["starts"]).to(device)
+        mask = t(c["mask"]) if "mask" in c else None
+        out = gqa_decode(q, k, v, lens, float(c["scale"]), kv_start=starts, mask=mask)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu(), c["out"], f"golden {name}")
+        if mask is not None:
+            out2 = gqa_decode_masked(q, k, v, mask, float(c["scale"]))
+            torch.cuda.synchronize()
+            assert_close(out2.float().cpu(), c["out"], f"golden {name} (masked entry)")
