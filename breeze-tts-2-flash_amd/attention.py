@@ -181,3 +181,59 @@ def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
         kernels.check(kernels.load().bz_gqa_decode_masked(ctypes.byref(a), ctypes.c_void_p(stream)),
                       "bz_gqa_decode_masked")
     return out
+
+
+def gqa_decode_fused(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
+                     cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     cache_pos: torch.Tensor, scale: float, out: torch.Tensor | None = None, *,
+                     seq_lens: torch.Tensor | None = None, kv_start: torch.Tensor | None = None,
+                     mask: torch.Tensor | None = None, num_splits: int = 0, max_seq_len: int = 0,
+                     combine: str | int = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused decode step (bz_gqa_decode_fused; the reference's attn_decode_fused, bb_attn.cu:433-460).
+
+    qkv: [B, (NH + 2 NKV) * D] bf16 raw q | k | v projections; q_norm_weight, k_norm_weight: [D] bf16; cos, sin:
+    [B, D] or [B, 1, D] bf16; cache_pos: int64 device tensor whose first element is the cache slot that receives the
+    new k (q_norm/k_norm + RoPE applied) and v of every row. Then attends like gqa_decode over [kv_start, seq_lens),
+    or, with seq_lens=None, over the interval of `mask` (required then). head_dim 128.
+    """
+    _check(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.dtype == torch.bfloat16,
+           "qkv must be a bf16 [B, (NH + 2 NKV) * D] tensor with a contiguous last dim")
+    _check(k_cache.dim() == 4, "k_cache must be [B, NKV, capacity, D]")
+    B, NKV, D = qkv.size(0), k_cache.size(1), k_cache.size(3)
+    NH = qkv.size(1) // D - 2 * NKV
+    _check(NH > 0 and qkv.size(1) == (NH + 2 * NKV) * D, f"qkv width {qkv.size(1)} is not (NH + 2*{NKV}) * {D}")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        _check(w.dtype == torch.bfloat16 and w.numel() == D and w.is_contiguous() and w.device == qkv.device,
+               f"{name} must be a contiguous bf16 [{D}] tensor on the qkv device")
+    for name, t in (("cos", cos), ("sin", sin)):
+        _check(t.dtype == torch.bfloat16 and t.stride(-1) == 1 and t.size(0) == B and t.size(-1) == D and
+               t.numel() == B * D and t.device == qkv.device, f"{name} must be bf16 [B, D] or [B, 1, D]")
+    _check(cos.stride(0) == sin.stride(0), "cos and sin must share their batch stride")
+    _check(cache_pos.dtype == torch.int64 and cache_pos.numel() >= 1 and cache_pos.device == qkv.device,
+           "cache_pos must be an int64 device tensor")
+    q_view = qkv[:, :NH * D].view(B, NH, D)
+    a, out = _fill_args(q_view, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
+    dev = qkv.device
+    if seq_lens is not None:
+        a.seq_lens = _int32_rows(seq_lens, B, "seq_lens", dev).data_ptr()
+        a.kv_start = _int32_rows(kv_start, B, "kv_start", dev).data_ptr() if kv_start is not None else None
+    else:
+        _check(mask is not None, "gqa_decode_fused needs seq_lens or an interval mask")
+    if mask is not None:
+        _check(mask.device == dev, "mask must be on the qkv device")
+        a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
+        a.mask = mask.data_ptr()
+    f = kernels.GqaDecodeFusedArgs()
+    f.base = a
+    f.qkv, f.qkv_stride_b = qkv.data_ptr(), qkv.stride(0)
+    f.q_norm_weight, f.k_norm_weight, f.eps = q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(eps)
+    f.cos, f.sin, f.rope_stride_b = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+    f.cache_pos = cache_pos.data_ptr()
+    with torch.cuda.device(dev):
+        ws = workspace if workspace is not None else get_workspace(
+            dev, a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity, a.num_splits, a.max_seq_len)
+        f.base.workspace, f.base.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        kernels.check(kernels.load().bz_gqa_decode_fused(ctypes.byref(f), ctypes.c_void_p(stream)),
+                      "bz_gqa_decode_fused")
+    return out

@@ -1,27 +1,6 @@
-// GQA flash-decoding attention for one decode step (q_len == 1) against a bf16 KV cache, written for gfx950
-// (MI355X, CDNA4: wave64, 256 CUs in 8 XCDs, HBM3E).
-//
-// What it computes is the reference's decode attention (flash/csrc/bb_attn.cu:1-17, the eager chain of
-// third_party/breeze-tts/models/breeze.py:259-286 with the head map of repeat_kv, :245-256): for each row b and
-// q head h, softmax(scale * q . K^T + mask) . V over the KV positions [kv_start[b], seq_lens[b]) of KV head
-// h / G. The arithmetic is fp32 throughout (the north-star oracle), not the reference's bf16 rounding chain.
-//
-// Work decomposition (split-K over the KV length, "flash-decoding"):
-//   grid (splits, num_kv_heads, batch), 256 threads = 4 wave64 per workgroup.
-//   Each row's valid length is cut on the device into nact <= splits chunks of
-//   chunk = max(min_chunk, ceil(len / splits)) positions, so a fixed grid serves every length (HIP-graph safe) and
-//   the work follows the real length: workgroups past nact exit at once.
-//   A workgroup streams its chunk in tiles of ROWS * PPT positions. A KV row of head_dim bf16 is read by
-//   LPR = head_dim / 8 consecutive lanes, 16 bytes each, so one wave64 load instruction covers 64 * 16 B of
-//   consecutive positions (fully coalesced) and every K/V byte is read once, by one lane, straight into VGPRs.
-//   All G q heads of the GQA group use the same K/V registers.
-//   q . k: 8 fp32 FMAs per lane, then a 16- (or 8-) lane sum with DPP row permutations (no LDS traffic).
-//   Softmax: online, base 2 (scale * log2(e) folded into q), one running (max, sum, acc) per 16-lane row, so the
-//   main loop has no cross-row communication. Rows are merged at the end (xor shuffles inside the wave, LDS across
-//   the 4 waves) with the log-sum-exp rule.
-//   One split (nact == 1): the workgroup writes the bf16 output directly.
-//   Several splits: each writes (acc[D], max, sum) in fp32 to the workspace; they are merged in split order either
-//   by the last workgroup of the (batch, kv head) to finish (atomic counter, one launch) or by a second kernel.
+// Host side of libbz_gqa_decode.so: the C ABI of include/bz_gqa_decode.h (argument checks, workspace layout, split
+// and tiling heuristics, launches) and the kernel table of the plain (non-fused) attention. The device code is in
+// gqa_kernels.cuh; the fused-prologue kernels are instantiated in gqa_fused.hip.
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -29,565 +8,14 @@
 #include <atomic>
 
 #include "bz_gqa_decode.h"
+#include "gqa_kernels.cuh"
 
 namespace {
 
-constexpr int kThreads = 256;  // 4 wave64
-constexpr int kWave = 64;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kMaxSplits = 256;
-constexpr int kMaxDevices = 64;
-constexpr int kCounterStride = 64;  // ints: one 256-byte line per arrival counter (atomics to one line serialize)
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kExcluded = -1e30f;  // mask values <= this exclude the position (bb_attn.cu:9-11, :115)
-
-struct Params {
-  const uint16_t* q;
-  int64_t q_sb, q_sh;
-  const uint16_t* k;
-  const uint16_t* v;
-  int64_t kv_sb, kv_sh, kv_ss;
-  const int32_t* seq_lens;
-  const int32_t* kv_start;
-  const void* mask;
-  int64_t m_sb;
-  float scale_log2;  // scale * log2(e)
-  uint16_t* out;
-  int64_t o_sb, o_sh;
-  int B, NH, NKV, cap, splits, min_chunk;
-  int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
-  float* part_acc;   // [B, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
-  float2* part_ml;   // [B, NH, splits]     (m, sum_p 2^(s_p - m))
-  int* counters;     // [B, NKV] x kCounterStride arrivals, reset by the merging workgroup
-};
-
-// ---------------------------------------------------------------------------------------------- helpers
-
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
-
-// fp32 -> bf16, round to nearest even; NaN stays NaN (quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ __forceinline__ void unpack8(const uint4& w, float f[8]) {
-  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
-  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
-  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
-  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-// c + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs, accumulated in fp32 (v_dot2c_f32_bf16)
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
-}
-
-// Sum over the LPR (8 or 16) consecutive lanes that hold one KV row; every lane of the row gets the same value
-// (each step adds a lane-permuted copy, and fp32 addition is commutative, so all lanes agree bit for bit).
-template <int LPR>
-__device__ __forceinline__ float row_sum(float x) {
-  static_assert(LPR == 8 || LPR == 16, "row_sum covers 8 or 16 lanes");
-  x += dpp<0xb1>(x);   // quad_perm [1,0,3,2]
-  x += dpp<0x4e>(x);   // quad_perm [2,3,0,1]
-  x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within each 8 lanes
-  if (LPR == 16) x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i within each 16 lanes
-  return x;
-}
-
-// Value of lane (lane ^ OFF) for OFF in {8, 16, 32}, all on the VALU: row_ror:8 inside each 16-lane row for 8;
-// v_permlane16_swap / v_permlane32_swap for 16 / 32. A swap of x with itself leaves, in one of its two results, this
-// lane's own value and, in the other, the partner's; XOR-ing both with the own bits keeps the partner's bits
-// whichever result holds which.
-template <int OFF>
-__device__ __forceinline__ float lane_xor(float x) {
-  static_assert(OFF == 8 || OFF == 16 || OFF == 32, "lane_xor: 8, 16 or 32");
-  if constexpr (OFF == 8) {
-    return dpp<0x128>(x);
-  } else {
-    const uint32_t u = __float_as_uint(x);
-    if constexpr (OFF == 16) {
-      const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-      return __uint_as_float(r[0] ^ r[1] ^ u);
-    } else {
-      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-      return __uint_as_float(r[0] ^ r[1] ^ u);
-    }
-  }
-}
-
-// Clamp the row's range so that no access can leave [0, capacity).
-__device__ __forceinline__ void row_range(const Params& p, int b, int& start, int& end) {
-  int e = p.seq_lens[b];
-  e = e < 0 ? 0 : (e > p.cap ? p.cap : e);
-  int s = p.kv_start ? p.kv_start[b] : 0;
-  s = s < 0 ? 0 : (s > e ? e : s);
-  start = s;
-  end = e;
-}
-
-// Positions per split and number of non-empty splits for a row of length len (>= 1 split even when empty, so
-// that someone writes the row's output).
-__device__ __forceinline__ int split_chunk(int len, int splits, int min_chunk) {
-  const int c = (len + splits - 1) / splits;
-  return c > min_chunk ? c : min_chunk;
-}
-__device__ __forceinline__ int split_count(int len, int chunk) { return len > 0 ? (len + chunk - 1) / chunk : 1; }
-
-template <int MK>
-__device__ __forceinline__ float load_mask(const void* m, int64_t off) {
-  if (MK == BZ_MASK_BF16) return bf16_to_f32(static_cast<const uint16_t*>(m)[off]);
-  return static_cast<const float*>(m)[off];
-}
-
-// Reductions over the wave: inside 16-lane rows with DPP (quad_perm x2, half mirror, mirror), then across rows with
-// the permlane swaps. Every lane ends with the same value.
-__device__ __forceinline__ float wave_max(float x) {
-  x = fmaxf(x, dpp<0xb1>(x));
-  x = fmaxf(x, dpp<0x4e>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  x = fmaxf(x, dpp<0x140>(x));
-  x = fmaxf(x, lane_xor<16>(x));
-  return fmaxf(x, lane_xor<32>(x));
-}
-__device__ __forceinline__ float wave_sum(float x) {
-  x = row_sum<16>(x);
-  x += lane_xor<16>(x);
-  return x + lane_xor<32>(x);
-}
-
-// Split partials cross workgroups (and XCDs, each with its own L2) inside one launch, so they are written and read
-// as agent-scope relaxed atomics: on gfx950 these are sc1 accesses that write through to, and read from, the level
-// where all XCDs are coherent, with no L2 writeback or invalidate of the whole cache.
-__device__ __forceinline__ void st_agent(float* ptr, float v) {
-  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* ptr) {
-  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
-// Every load the merge needs is issued before anything waits: each thread's first kBatch split partials for its kOut
-// (q head, dim) outputs, and the (max, sum) pairs of q head `wave` (one lane per split). Split weights
-// w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s are reduced over the wave with DPP and lane swaps and stored to LDS
-// zero-padded, so the weighted sum over the first kBatch splits needs no per-split condition.
-template <int D, int G, int NT>
-__device__ void merge_splits(const Params& p, int b, int h, int nact) {
-  constexpr int kBatch = 32;
-  constexpr int NW = NT / kWave;
-  constexpr int kOut = (G * D + NT - 1) / NT;
-  constexpr int kPerLane = kMaxSplits / kWave;
-  __shared__ __align__(16) float s_w[G][kMaxSplits];
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int64_t row0 = (int64_t)b * p.NH + h * G;  // first q head of the group, as a [B * NH] row index
-
-  float t[kOut][kBatch];
-#pragma unroll
-  for (int k = 0; k < kOut; ++k) {
-    const int o = tid + k * NT;
-    if (o < G * D) {
-      const float* pa = p.part_acc + (row0 + o / D) * p.splits * D + o % D;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) t[k][u] = (u < nact) ? ld_agent(pa + (int64_t)u * D) : 0.f;
-    }
-  }
-  float mv[kPerLane], lv[kPerLane];
-  auto load_ml = [&](int g) {
-    const float* ml = reinterpret_cast<const float*>(p.part_ml + (row0 + g) * p.splits);
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-      const int s = lane + kWave * j;
-      mv[j] = (s < nact) ? ld_agent(ml + 2 * s) : -INFINITY;
-      lv[j] = (s < nact) ? ld_agent(ml + 2 * s + 1) : 0.f;
-    }
-  };
-  if (wave < G) load_ml(wave);
-
-  for (int g = wave; g < G; g += NW) {
-    if (g != wave) load_ml(g);
-    float mloc = mv[0];
-#pragma unroll
-    for (int j = 1; j < kPerLane; ++j) mloc = fmaxf(mloc, mv[j]);
-    const float M = wave_max(mloc);
-    const float mu = (M == -INFINITY) ? 0.f : M;
-    float lloc = 0.f;
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-      mv[j] = fast_exp2(mv[j] - mu);  // 0 for the padding (-inf)
-      lloc = fmaf(mv[j], lv[j], lloc);
-    }
-    const float L = wave_sum(lloc);
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) s_w[g][lane + kWave * j] = mv[j] * inv;
-  }
-  __syncthreads();
-
-#pragma unroll
-  for (int k = 0; k < kOut; ++k) {
-    const int o = tid + k * NT;
-    if (o >= G * D) continue;
-    const int g = o / D, d = o % D;
-    const float* pa = p.part_acc + (row0 + g) * p.splits * D + d;
-    float a = 0.f;
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][u], t[k][u], a);
-    for (int s0 = kBatch; s0 < nact; s0 += kBatch) {
-      float x[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) x[u] = (s0 + u < nact) ? ld_agent(pa + (int64_t)(s0 + u) * D) : 0.f;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][s0 + u], x[u], a);
-    }
-    p.out[(int64_t)b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
-  }
-}
-
-// One tile of KV rows held in VGPRs: position pos0 + ROWS * i for i < PPT (pos0 = tile start + this lane's row).
-template <int PPT>
-struct Tile {
-  uint4 k[PPT], v[PPT];
-  float m[PPT];
-};
-
-// Issue every K and V load of a tile (and its mask values) before any arithmetic. Positions >= hi are not read.
-template <int ROWS, int PPT, int MK>
-__device__ __forceinline__ void load_tile(Tile<PPT>& t, const uint16_t* kb, const uint16_t* vb, int64_t ss,
-                                          const void* mask, int64_t mrow, int pos0, int hi) {
-#pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-    const int pos = pos0 + ROWS * i;
-    if (pos < hi) {
-      t.k[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)pos * ss);
-      t.v[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)pos * ss);
-    } else {
-      t.k[i] = make_uint4(0, 0, 0, 0);
-      t.v[i] = make_uint4(0, 0, 0, 0);
-    }
-    if (MK != BZ_MASK_NONE) t.m[i] = (pos < hi) ? load_mask<MK>(mask, mrow + pos) : 0.f;
-  }
-}
-
-// Fold one tile into the running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP row sum,
-// scaled by scale * log2(e); online softmax in base 2 with one max per wave (m is wave-uniform, l and acc per row);
-// then P.V in fp32 on the unpacked V registers.
-// A slot whose row lies past hi is skipped (the condition is uniform over the row's lanes, so the DPP sum, which
-// reads only lanes of the same row, never sees a skipped lane).
-template <int LPR, int ROWS, int G, int PPT, int MK>
-__device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G], float scale_log2, float (&m)[G],
-                                             float (&l)[G], float (&acc)[G][8], int pos0, int hi) {
-  float s[G][PPT];
-#pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) s[g][i] = -INFINITY;
-    const int pos = pos0 + ROWS * i;
-    if (pos < hi) {
-      bool inc = true;
-      if (MK != BZ_MASK_NONE) {
-        inc = t.m[i] > kExcluded;
-        // an excluded position must not touch the accumulator even through 0 * V (V may hold NaN there)
-        if (!inc) t.v[i] = make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = dot2_bf16(qp[g].x, t.k[i].x, 0.f);
-        d = dot2_bf16(qp[g].y, t.k[i].y, d);
-        d = dot2_bf16(qp[g].z, t.k[i].z, d);
-        d = dot2_bf16(qp[g].w, t.k[i].w, d);
-        d = row_sum<LPR>(d) * scale_log2;
-        if (MK != BZ_MASK_NONE) d = fmaf(t.m[i], kLog2e, d);
-        if (inc) s[g][i] = d;
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float mt = s[g][0];
-#pragma unroll
-    for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
-    // one running max per wave: the rows of a wave can then be merged by plain sums
-    if (LPR == 8) mt = fmaxf(mt, lane_xor<8>(mt));
-    mt = fmaxf(mt, lane_xor<16>(mt));
-    mt = fmaxf(mt, lane_xor<32>(mt));
-    const float mn = fmaxf(m[g], mt);
-    const float mu = (mn == -INFINITY) ? 0.f : mn;
-    const float alpha = fast_exp2(m[g] - mu);
-    l[g] *= alpha;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      s[g][i] = fast_exp2(s[g][i] - mu);
-      l[g] += s[g][i];
-    }
-    m[g] = mn;
-  }
-#pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-    if (pos0 + ROWS * i < hi) {
-      float vf[8];
-      unpack8(t.v[i], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
-    }
-  }
-}
-
-// Add lane (lane ^ OFF)'s (l, acc), which covers the same dims for other KV rows under the same wave-uniform max.
-// Both lanes end with the same sums.
-template <int OFF, int G>
-__device__ __forceinline__ void sum_rows(float (&l)[G], float (&acc)[G][8]) {
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] += lane_xor<OFF>(l[g]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] += lane_xor<OFF>(acc[g][j]);
-  }
-}
-
-// ---------------------------------------------------------------------------------------------- kernels
-
-template <int D, int G, int PPT, int MK, int NT>
-__global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
-  constexpr int NW = NT / kWave;        // waves per workgroup
-  constexpr int LPR = D / 8;            // lanes per KV row, 16 B (8 bf16) each
-  constexpr int ROWS = NT / LPR;        // KV rows per load instruction across the workgroup
-  constexpr int TP = ROWS * PPT;        // positions per tile
-  constexpr int RPW = kWave / LPR;      // rows per wave
-  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
-
-  // q of the G heads of this group, this lane's 8 dims: issued first, since it does not depend on the row's length
-  uint16_t qh[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint16_t* qsrc = p.q + (int64_t)b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + 8 * c;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qh[g][j] = qsrc[j];
-  }
-
-  int start, end;
-  row_range(p, b, start, end);
-  const int len = end - start;
-  const int chunk = split_chunk(len, p.splits, p.min_chunk);
-  const int nact = split_count(len, chunk);
-  if (split >= nact) return;
-  const int lo = start + split * chunk;
-  const int hi = min(lo + chunk, end);
-
-  const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + 8 * c;
-  const uint16_t* kb = p.k + head_off;
-  const uint16_t* vb = p.v + head_off;
-  const int64_t mrow = (int64_t)b * p.m_sb;
-
-  // The first tile's K/V loads (and, for PPT <= 4, the second's) go out before q is converted, so no wave waits on
-  // q before streaming. Tiles A and B ping-pong without register copies: while one is consumed the other's loads
-  // are in flight. Loads of positions >= hi are skipped, so a one-tile chunk issues no extra traffic.
-  constexpr bool kPingPong = PPT <= 4;
-  Tile<PPT> ta, tb;
-  load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, lo + r, hi);
-  if (kPingPong) load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, lo + TP + r, hi);
-
-  uint4 qp[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    qp[g].x = qh[g][0] | ((uint32_t)qh[g][1] << 16);
-    qp[g].y = qh[g][2] | ((uint32_t)qh[g][3] << 16);
-    qp[g].z = qh[g][4] | ((uint32_t)qh[g][5] << 16);
-    qp[g].w = qh[g][6] | ((uint32_t)qh[g][7] << 16);
-  }
-
-  float m[G], l[G], acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
-  }
-
-  if (kPingPong) {
-    for (int t0 = lo; t0 < hi; t0 += 2 * TP) {
-      consume_tile<LPR, ROWS, G, PPT, MK>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi);
-      if (t0 + TP >= hi) break;
-      load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + 2 * TP + r, hi);
-      consume_tile<LPR, ROWS, G, PPT, MK>(tb, qp, p.scale_log2, m, l, acc, t0 + TP + r, hi);
-      load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, t0 + 3 * TP + r, hi);
-    }
-  } else {
-    for (int t0 = lo; t0 < hi; t0 += TP) {
-      consume_tile<LPR, ROWS, G, PPT, MK>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi);
-      if (t0 + TP < hi) load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + TP + r, hi);
-    }
-  }
-
-  // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims)
-  if (LPR == 8) sum_rows<8, G>(l, acc);
-  sum_rows<16, G>(l, acc);
-  sum_rows<32, G>(l, acc);
-
-  // merge the NW waves through LDS
-  __shared__ float s_acc[NW][G][D];
-  __shared__ float s_m[NW][G], s_l[NW][G];
-  const int w = tid / kWave, lane = tid % kWave;
-  if (lane < LPR) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_acc[w][g][8 * c + j] = acc[g][j];
-      if (lane == 0) {
-        s_m[w][g] = m[g];
-        s_l[w][g] = l[g];
-      }
-    }
-  }
-  __syncthreads();
-  (void)RPW;
-
-  for (int o = tid; o < G * D; o += NT) {
-    const int g = o / D, d = o % D, hq = h * G + g;
-    float M = s_m[0][g];
-#pragma unroll
-    for (int u = 1; u < NW; ++u) M = fmaxf(M, s_m[u][g]);
-    const float mu = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f, A = 0.f;
-#pragma unroll
-    for (int u = 0; u < NW; ++u) {
-      const float e = fast_exp2(s_m[u][g] - mu);
-      L = fmaf(e, s_l[u][g], L);
-      A = fmaf(e, s_acc[u][g][d], A);
-    }
-    if (nact == 1) {
-      p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(L > 0.f ? A / L : 0.f);
-    } else {
-      const int64_t ps = ((int64_t)b * p.NH + hq) * p.splits + split;
-      st_agent(p.part_acc + ps * D + d, A);
-      if (d == 0) {
-        st_agent(reinterpret_cast<float*>(p.part_ml + ps), M);
-        st_agent(reinterpret_cast<float*>(p.part_ml + ps) + 1, L);
-      }
-    }
-  }
-  if (nact == 1 || !p.combine_last) return;
-
-  // Last-arriving workgroup of this (b, kv head) merges the splits. Each wave waits until its agent-scope partial
-  // stores have completed (s_waitcnt vmcnt(0); gfx9 encoding with expcnt/lgkmcnt left open), the barrier collects
-  // the waves, and thread 0 counts the workgroup in with one agent-scope RMW. The workgroup that brings the
-  // count to nact reads the partials with agent-scope loads; it resets the counter for the next call.
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0x0f70);
-  __syncthreads();
-  if (tid == 0) {
-    int* cnt = p.counters + (b * p.NKV + h) * kCounterStride;
-    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == nact - 1);
-    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  merge_splits<D, G, NT>(p, b, h, nact);
-}
-
-// Second-launch merge: one workgroup per (kv head, row).
-template <int D, int G>
-__global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
-  const int h = blockIdx.x, b = blockIdx.y;
-  int start, end;
-  row_range(p, b, start, end);
-  const int len = end - start;
-  const int nact = split_count(len, split_chunk(len, p.splits, p.min_chunk));
-  if (nact == 1) return;  // the split kernel wrote the output
-  merge_splits<D, G, kThreads>(p, b, h, nact);
-}
-
-// Interval of the additive mask row: first and last position with value > -1e30.
-template <int MK>
-__global__ void __launch_bounds__(kThreads) mask_range_kernel(const void* mask, int64_t m_sb, int cap,
-                                                              int32_t* start, int32_t* end) {
-  const int b = blockIdx.x, tid = threadIdx.x;
-  int lo = cap, hi = -1;
-  for (int pos = tid; pos < cap; pos += kThreads) {
-    if (load_mask<MK>(mask, (int64_t)b * m_sb + pos) > kExcluded) {
-      lo = min(lo, pos);
-      hi = max(hi, pos);
-    }
-  }
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    lo = min(lo, __shfl_xor(lo, off));
-    hi = max(hi, __shfl_xor(hi, off));
-  }
-  __shared__ int s_lo[kWaves], s_hi[kWaves];
-  if (tid % kWave == 0) {
-    s_lo[tid / kWave] = lo;
-    s_hi[tid / kWave] = hi;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    for (int u = 1; u < kWaves; ++u) {
-      lo = min(lo, s_lo[u]);
-      hi = max(hi, s_hi[u]);
-    }
-    const bool any = hi >= 0;
-    start[b] = any ? lo : 0;
-    end[b] = any ? hi + 1 : 0;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------- host side
-
-using SplitFn = void (*)(const Params);
-
-template <int D, int G, int MK, int NT>
-SplitFn pick_ppt(int ppt) {
-  switch (ppt) {
-    case 1: return gqa_split_kernel<D, G, 1, MK, NT>;
-    case 2: return gqa_split_kernel<D, G, 2, MK, NT>;
-    default: return gqa_split_kernel<D, G, 4, MK, NT>;
-  }
-}
-
-template <int D, int G, int NT>
-SplitFn pick_mask(int mk, int ppt) {
-  switch (mk) {
-    case BZ_MASK_BF16: return pick_ppt<D, G, BZ_MASK_BF16, NT>(ppt);
-    case BZ_MASK_F32: return pick_ppt<D, G, BZ_MASK_F32, NT>(ppt);
-    default: return pick_ppt<D, G, BZ_MASK_NONE, NT>(ppt);
-  }
-}
-
-template <int D, int NT>
-SplitFn pick_group(int G, int mk, int ppt) {
-  switch (G) {
-    case 1: return pick_mask<D, 1, NT>(mk, ppt);
-    case 2: return pick_mask<D, 2, NT>(mk, ppt);
-    case 4: return pick_mask<D, 4, NT>(mk, ppt);
-    case 8: return pick_mask<D, 8, NT>(mk, ppt);
-    default: return nullptr;
-  }
-}
-
-SplitFn pick_split(int D, int G, int mk, int ppt, int nt) {
-  if (D == 128) return nt == 512 ? pick_group<128, 512>(G, mk, ppt) : pick_group<128, 256>(G, mk, ppt);
-  if (D == 64) return nt == 512 ? pick_group<64, 512>(G, mk, ppt) : pick_group<64, 256>(G, mk, ppt);
+SplitFn pick_split(int D, int G, int mk, int ppt, int nt, bool fused) {
+  if (fused) return bz::pick_split_fused(D, G, mk, ppt, nt);
+  if (D == 128) return nt == 512 ? pick_group<128, 512, false>(G, mk, ppt) : pick_group<128, 256, false>(G, mk, ppt);
+  if (D == 64) return nt == 512 ? pick_group<64, 512, false>(G, mk, ppt) : pick_group<64, 256, false>(G, mk, ppt);
   return nullptr;
 }
 
@@ -704,8 +132,10 @@ int resolve_splits(const bz_gqa_decode_args* a, int* splits) {
   return BZ_OK;
 }
 
+// Checks the workspace, picks the kernels and launches the split kernel (and, on request, the merge kernel).
+// f != nullptr selects the fused-prologue variant.
 int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
-           int mask_kind) {
+           int mask_kind, const bz_gqa_decode_fused_args* f) {
   const int B = a->batch, NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
   const int G = NH / NKV;
   int splits = 0;
@@ -725,7 +155,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   if (rc != BZ_OK) return rc;
   const int nt = threads_for(D, G, chunk, (int64_t)splits * NKV * B, cus);
   const int ppt = ppt_for(D, G, chunk, nt);
-  SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt);
+  SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt, f != nullptr);
   SplitFn comb_fn = pick_combine(D, G);
   if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
 
@@ -758,6 +188,26 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   p.part_acc = reinterpret_cast<float*>(wsb + ws.acc);
   p.part_ml = reinterpret_cast<float2*>(wsb + ws.ml);
   p.counters = reinterpret_cast<int*>(wsb + ws.counters);
+  p.qkv = nullptr;
+  p.qkv_sb = 0;
+  p.qn_w = p.kn_w = p.cos = p.sin = nullptr;
+  p.eps = 0.f;
+  p.cs_sb = 0;
+  p.cache_pos = nullptr;
+  p.k_out = p.v_out = nullptr;
+  if (f != nullptr) {
+    p.qkv = static_cast<const uint16_t*>(f->qkv);
+    p.qkv_sb = f->qkv_stride_b;
+    p.qn_w = static_cast<const uint16_t*>(f->q_norm_weight);
+    p.kn_w = static_cast<const uint16_t*>(f->k_norm_weight);
+    p.eps = f->eps;
+    p.cos = static_cast<const uint16_t*>(f->cos);
+    p.sin = static_cast<const uint16_t*>(f->sin);
+    p.cs_sb = f->rope_stride_b;
+    p.cache_pos = f->cache_pos;
+    p.k_out = const_cast<uint16_t*>(p.k);
+    p.v_out = const_cast<uint16_t*>(p.v);
+  }
 
   hipLaunchKernelGGL(split_fn, dim3(splits, NKV, B), dim3(nt), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
@@ -768,9 +218,10 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   return BZ_OK;
 }
 
-int check_common(const bz_gqa_decode_args* a) {
+int check_common(const bz_gqa_decode_args* a, bool need_q) {
   if (a == nullptr) return BZ_ERR_NULL;
-  if (a->q == nullptr || a->k_cache == nullptr || a->v_cache == nullptr || a->out == nullptr) return BZ_ERR_NULL;
+  if ((need_q && a->q == nullptr) || a->k_cache == nullptr || a->v_cache == nullptr || a->out == nullptr)
+    return BZ_ERR_NULL;
   int rc = check_sizes(a->batch, a->num_q_heads, a->num_kv_heads, a->head_dim, a->capacity);
   if (rc != BZ_OK) return rc;
   const uintptr_t kp = reinterpret_cast<uintptr_t>(a->k_cache), vp = reinterpret_cast<uintptr_t>(a->v_cache);
@@ -781,41 +232,84 @@ int check_common(const bz_gqa_decode_args* a) {
   return BZ_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-__attribute__((visibility("default"))) int bz_gqa_decode(const bz_gqa_decode_args* a, hipStream_t stream) {
-  int rc = check_common(a);
-  if (rc != BZ_OK) return rc;
-  if (a->seq_lens == nullptr) return BZ_ERR_NULL;
-  const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
-  if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
-  return launch(a, stream, a->seq_lens, a->kv_start, mk);
-}
-
-__attribute__((visibility("default"))) int bz_gqa_decode_masked(const bz_gqa_decode_args* a, hipStream_t stream) {
-  int rc = check_common(a);
-  if (rc != BZ_OK) return rc;
+// Launch the mask-interval kernel into the workspace's ranges segment; returns the [start, end) arrays.
+int mask_ranges(const bz_gqa_decode_args* a, hipStream_t stream, int32_t** start, int32_t** end) {
   if (a->mask == nullptr) return BZ_ERR_NULL;
   if (a->mask_dtype != BZ_MASK_BF16 && a->mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
   int splits = 0;
-  rc = resolve_splits(a, &splits);
+  int rc = resolve_splits(a, &splits);
   if (rc != BZ_OK) return rc;
   const WsLayout ws = ws_layout(a->batch, a->num_q_heads, a->num_kv_heads, a->head_dim, splits);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
   int32_t* ranges = reinterpret_cast<int32_t*>(static_cast<char*>(a->workspace) + ws.ranges);
-  int32_t* start = ranges;
-  int32_t* end = ranges + a->batch;
+  *start = ranges;
+  *end = ranges + a->batch;
   if (a->mask_dtype == BZ_MASK_BF16)
     hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_BF16>, dim3(a->batch), dim3(kThreads), 0, stream, a->mask,
-                       a->mask_stride_b, a->capacity, start, end);
+                       a->mask_stride_b, a->capacity, *start, *end);
   else
     hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_F32>, dim3(a->batch), dim3(kThreads), 0, stream, a->mask,
-                       a->mask_stride_b, a->capacity, start, end);
+                       a->mask_stride_b, a->capacity, *start, *end);
   if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
-  return launch(a, stream, end, start, a->mask_dtype);
+  return BZ_OK;
+}
+
+int check_fused(const bz_gqa_decode_fused_args* f) {
+  if (f == nullptr) return BZ_ERR_NULL;
+  const bz_gqa_decode_args* a = &f->base;
+  int rc = check_common(a, false);
+  if (rc != BZ_OK) return rc;
+  if (f->qkv == nullptr || f->q_norm_weight == nullptr || f->k_norm_weight == nullptr || f->cos == nullptr ||
+      f->sin == nullptr || f->cache_pos == nullptr)
+    return BZ_ERR_NULL;
+  if (a->head_dim != 128) return BZ_ERR_UNSUPPORTED;
+  if (f->qkv_stride_b < (int64_t)(a->num_q_heads + 2 * a->num_kv_heads) * a->head_dim) return BZ_ERR_SHAPE;
+  if (f->rope_stride_b < a->head_dim) return BZ_ERR_SHAPE;
+  const uintptr_t ptrs = reinterpret_cast<uintptr_t>(f->qkv) | reinterpret_cast<uintptr_t>(f->q_norm_weight) |
+                         reinterpret_cast<uintptr_t>(f->k_norm_weight) | reinterpret_cast<uintptr_t>(f->cos) |
+                         reinterpret_cast<uintptr_t>(f->sin);
+  if ((ptrs & 15) || ((f->qkv_stride_b | f->rope_stride_b) & 7)) return BZ_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(f->cache_pos) & 7)) return BZ_ERR_ALIGNMENT;
+  return BZ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int bz_gqa_decode(const bz_gqa_decode_args* a, hipStream_t stream) {
+  int rc = check_common(a, true);
+  if (rc != BZ_OK) return rc;
+  if (a->seq_lens == nullptr) return BZ_ERR_NULL;
+  const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
+  if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
+  return launch(a, stream, a->seq_lens, a->kv_start, mk, nullptr);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_masked(const bz_gqa_decode_args* a, hipStream_t stream) {
+  int rc = check_common(a, true);
+  if (rc != BZ_OK) return rc;
+  int32_t *start = nullptr, *end = nullptr;
+  rc = mask_ranges(a, stream, &start, &end);
+  if (rc != BZ_OK) return rc;
+  return launch(a, stream, end, start, a->mask_dtype, nullptr);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* f,
+                                                               hipStream_t stream) {
+  int rc = check_fused(f);
+  if (rc != BZ_OK) return rc;
+  const bz_gqa_decode_args* a = &f->base;
+  if (a->seq_lens != nullptr) {
+    const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
+    if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
+    return launch(a, stream, a->seq_lens, a->kv_start, mk, f);
+  }
+  int32_t *start = nullptr, *end = nullptr;
+  rc = mask_ranges(a, stream, &start, &end);
+  if (rc != BZ_OK) return rc;
+  return launch(a, stream, end, start, a->mask_dtype, f);
 }
 
 __attribute__((visibility("default"))) int bz_gqa_decode_workspace_size(int32_t batch, int32_t num_q_heads,
@@ -855,7 +349,8 @@ __attribute__((visibility("default"))) const char* bz_status_string(int status) 
     case BZ_OK: return "ok";
     case BZ_ERR_NULL: return "a required pointer is NULL";
     case BZ_ERR_SHAPE: return "a size is out of range (or num_q_heads is not a multiple of num_kv_heads)";
-    case BZ_ERR_UNSUPPORTED: return "unsupported head_dim (64, 128) or GQA group size (1, 2, 4, 8)";
+    case BZ_ERR_UNSUPPORTED:
+      return "unsupported head_dim (64, 128; 128 for the fused prologue) or GQA group size (1, 2, 4, 8)";
     case BZ_ERR_ALIGNMENT: return "K/V pointers and strides must be 16-byte aligned, workspace 256-byte aligned";
     case BZ_ERR_WORKSPACE: return "workspace missing or smaller than bz_gqa_decode_workspace_size()";
     case BZ_ERR_MASK_DTYPE: return "mask_dtype must be BZ_MASK_BF16 or BZ_MASK_F32 when a mask is given";

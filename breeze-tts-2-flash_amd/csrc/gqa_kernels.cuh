@@ -1,0 +1,706 @@
+// Device code of the MI355X (gfx950) GQA flash-decoding attention, shared by the translation units of
+// libbz_gqa_decode.so (gqa_decode.hip: C ABI and plain kernels; gqa_fused.hip: kernels with the fused prologue).
+//
+// What it computes is the reference's decode attention (flash/csrc/bb_attn.cu:1-17, the eager chain of
+// third_party/breeze-tts/models/breeze.py:259-286 with the head map of repeat_kv, :245-256): for each row b and
+// q head h, softmax(scale * q . K^T + mask) . V over the KV positions [kv_start[b], seq_lens[b]) of KV head
+// h / G, in fp32 (the north-star oracle), not the reference's bf16 rounding chain. The fused variant first applies
+// the reference's prologue (bb_attn.cu:78-149): q_norm / k_norm (Qwen3 RMSNorm) and RoPE on the raw projections at
+// the eager bf16 rounding points, and writes the new k and v into cache slot cache_pos.
+//
+// Work decomposition (split-K over the KV length, "flash-decoding"):
+//   grid (splits, num_kv_heads, batch), NT = 256 or 512 threads (4 or 8 wave64) per workgroup.
+//   Each row's valid length is cut on the device into nact <= splits chunks of
+//   chunk = max(min_chunk, ceil(len / splits)) positions, so a fixed grid serves every length (HIP-graph safe) and
+//   the work follows the real length: workgroups past nact exit at once.
+//   A workgroup streams its chunk in tiles of ROWS * PPT positions, two tiles in flight (ping-pong). A KV row of
+//   head_dim bf16 is read by LPR = head_dim / 8 consecutive lanes, 16 bytes each, so one wave64 load instruction
+//   covers 64 * 16 B of consecutive positions and every K/V byte is read once, by one lane, straight into VGPRs.
+//   All G q heads of the GQA group use the same K/V registers.
+//   q . k: four v_dot2c_f32_bf16 per head on the packed bf16 words, then a 16- (or 8-) lane DPP row sum.
+//   Softmax: online, base 2 (scale * log2(e) applied to the score), one running max per wave (the rows of a wave
+//   take the tile max across rows with lane swaps), per-row running sums and accumulators. At the end of the chunk
+//   the rows of a wave are summed with lane swaps and the waves are merged through LDS (log-sum-exp rule).
+//   One chunk (nact == 1): the workgroup writes the bf16 output directly. Several: each writes (acc[D], max, sum) in
+//   fp32 to the workspace and the last workgroup of the (batch, kv head) to arrive merges them in split order (or,
+//   on request, a second kernel does).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "bz_gqa_decode.h"
+
+namespace bz {
+
+struct Params {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_sb, kv_sh, kv_ss;
+  const int32_t* seq_lens;
+  const int32_t* kv_start;
+  const void* mask;
+  int64_t m_sb;
+  float scale_log2;  // scale * log2(e)
+  uint16_t* out;
+  int64_t o_sb, o_sh;
+  int B, NH, NKV, cap, splits, min_chunk;
+  int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
+  float* part_acc;   // [B, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
+  float2* part_ml;   // [B, NH, splits]     (m, sum_p 2^(s_p - m))
+  int* counters;     // [B, NKV] x kCounterStride arrivals, reset by the merging workgroup
+  // fused prologue only
+  const uint16_t* qkv;  // [B, (NH + 2 NKV) * D] raw projections: q heads | k heads | v heads
+  int64_t qkv_sb;
+  const uint16_t* qn_w;  // [D]
+  const uint16_t* kn_w;  // [D]
+  float eps;
+  const uint16_t* cos;  // [B, D]
+  const uint16_t* sin;
+  int64_t cs_sb;
+  const int64_t* cache_pos;  // device scalar: cache slot of the new k / v
+  uint16_t* k_out;  // the caches, written at cache_pos
+  uint16_t* v_out;
+};
+
+using SplitFn = void (*)(const Params);
+
+// Kernel tables (gqa_fused.hip defines the fused one).
+SplitFn pick_split_fused(int D, int G, int mk, int ppt, int nt);
+
+}  // namespace bz
+
+namespace {
+
+using bz::Params;
+using bz::SplitFn;
+
+
+constexpr int kThreads = 256;  // 4 wave64 (merge and mask kernels)
+constexpr int kWave = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxSplits = 256;
+constexpr int kMaxDevices = 64;
+constexpr int kCounterStride = 64;  // ints: one 256-byte line per arrival counter (atomics to one line serialize)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kExcluded = -1e30f;  // mask values <= this exclude the position (bb_attn.cu:9-11, :115)
+
+// ---------------------------------------------------------------------------------------------- helpers
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& w, float f[8]) {
+  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// c + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs, accumulated in fp32 (v_dot2c_f32_bf16)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over the LPR (8 or 16) consecutive lanes that hold one KV row; every lane of the row gets the same value
+// (each step adds a lane-permuted copy, and fp32 addition is commutative, so all lanes agree bit for bit).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+  static_assert(LPR == 8 || LPR == 16, "row_sum covers 8 or 16 lanes");
+  x += dpp<0xb1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4e>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within each 8 lanes
+  if (LPR == 16) x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i within each 16 lanes
+  return x;
+}
+
+// Value of lane (lane ^ OFF) for OFF in {8, 16, 32}, all on the VALU: row_ror:8 inside each 16-lane row for 8;
+// v_permlane16_swap / v_permlane32_swap for 16 / 32. A swap of x with itself leaves, in one of its two results, this
+// lane's own value and, in the other, the partner's; XOR-ing both with the own bits keeps the partner's bits
+// whichever result holds which.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float x) {
+  static_assert(OFF == 8 || OFF == 16 || OFF == 32, "lane_xor: 8, 16 or 32");
+  if constexpr (OFF == 8) {
+    return dpp<0x128>(x);
+  } else {
+    const uint32_t u = __float_as_uint(x);
+    if constexpr (OFF == 16) {
+      const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      return __uint_as_float(r[0] ^ r[1] ^ u);
+    } else {
+      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      return __uint_as_float(r[0] ^ r[1] ^ u);
+    }
+  }
+}
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// Value of the lane holding the same 8 dims +/- head_dim / 2 (rotate_half's partner): LPR / 2 lanes away inside the
+// row; row_ror:8 for head_dim 128, a bpermute for head_dim 64.
+template <int LPR>
+__device__ __forceinline__ float half_partner(float x) {
+  if constexpr (LPR == 16) return lane_xor<8>(x);
+  else return __shfl_xor(x, LPR / 2);
+}
+
+// Qwen3 per-head RMSNorm then RoPE on this lane's 8 dims (dims 8c .. 8c + 7 of a head spread over LPR lanes), at the
+// eager rounding points of transformers' Qwen3RMSNorm + apply_rotary_pos_emb, which bb_attn.cu:78-100 reproduces:
+//   h = bf16(x * rsqrt(mean(x^2) + eps));  y = bf16(w * h);
+//   out = bf16(bf16(y * cos) + bf16(rotate_half(y) * sin)),  rotate_half(y) = [-y[D/2:], y[:D/2]].
+// Returns the 8 results as packed bf16 pairs.
+template <int LPR>
+__device__ __forceinline__ uint4 norm_rope8(const uint4& xr, const uint4& wr, const uint4& cr, const uint4& sr,
+                                            float eps, int c) {
+  float x[8], w[8], cs[8], sn[8];
+  unpack8(xr, x);
+  unpack8(wr, w);
+  unpack8(cr, cs);
+  unpack8(sr, sn);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
+  ss = row_sum<LPR>(ss);
+  const float inv_rms = rsqrtf(ss * (1.f / (8 * LPR)) + eps);
+  float y[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = round_bf16(w[j] * round_bf16(x[j] * inv_rms));
+  const bool first_half = c < LPR / 2;
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float partner = half_partner<LPR>(y[j]);
+    const float rot = first_half ? -partner : partner;
+    o[j] = round_bf16(y[j] * cs[j]) + round_bf16(rot * sn[j]);
+  }
+  return make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                    pack_bf16x2(o[6], o[7]));
+}
+
+// Clamp the row's range so that no access can leave [0, capacity).
+__device__ __forceinline__ void row_range(const Params& p, int b, int& start, int& end) {
+  int e = p.seq_lens[b];
+  e = e < 0 ? 0 : (e > p.cap ? p.cap : e);
+  int s = p.kv_start ? p.kv_start[b] : 0;
+  s = s < 0 ? 0 : (s > e ? e : s);
+  start = s;
+  end = e;
+}
+
+// Positions per split and number of non-empty splits for a row of length len (>= 1 split even when empty, so
+// that someone writes the row's output).
+__device__ __forceinline__ int split_chunk(int len, int splits, int min_chunk) {
+  const int c = (len + splits - 1) / splits;
+  return c > min_chunk ? c : min_chunk;
+}
+__device__ __forceinline__ int split_count(int len, int chunk) { return len > 0 ? (len + chunk - 1) / chunk : 1; }
+
+template <int MK>
+__device__ __forceinline__ float load_mask(const void* m, int64_t off) {
+  if (MK == BZ_MASK_BF16) return bf16_to_f32(static_cast<const uint16_t*>(m)[off]);
+  return static_cast<const float*>(m)[off];
+}
+
+// Reductions over the wave: inside 16-lane rows with DPP (quad_perm x2, half mirror, mirror), then across rows with
+// the permlane swaps. Every lane ends with the same value.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp<0xb1>(x));
+  x = fmaxf(x, dpp<0x4e>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  x = fmaxf(x, lane_xor<16>(x));
+  return fmaxf(x, lane_xor<32>(x));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row_sum<16>(x);
+  x += lane_xor<16>(x);
+  return x + lane_xor<32>(x);
+}
+
+// Split partials cross workgroups (and XCDs, each with its own L2) inside one launch, so they are written and read
+// as agent-scope relaxed atomics: on gfx950 these are sc1 accesses that write through to, and read from, the level
+// where all XCDs are coherent, with no L2 writeback or invalidate of the whole cache.
+__device__ __forceinline__ void st_agent(float* ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* ptr) {
+  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
+// Every load the merge needs is issued before anything waits: each thread's first kBatch split partials for its kOut
+// (q head, dim) outputs, and the (max, sum) pairs of q head `wave` (one lane per split). Split weights
+// w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s are reduced over the wave with DPP and lane swaps and stored to LDS
+// zero-padded, so the weighted sum over the first kBatch splits needs no per-split condition.
+template <int D, int G, int NT>
+__device__ void merge_splits(const Params& p, int b, int h, int nact) {
+  constexpr int kBatch = 32;
+  constexpr int NW = NT / kWave;
+  constexpr int kOut = (G * D + NT - 1) / NT;
+  constexpr int kPerLane = kMaxSplits / kWave;
+  __shared__ __align__(16) float s_w[G][kMaxSplits];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int64_t row0 = (int64_t)b * p.NH + h * G;  // first q head of the group, as a [B * NH] row index
+
+  float t[kOut][kBatch];
+#pragma unroll
+  for (int k = 0; k < kOut; ++k) {
+    const int o = tid + k * NT;
+    if (o < G * D) {
+      const float* pa = p.part_acc + (row0 + o / D) * p.splits * D + o % D;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) t[k][u] = (u < nact) ? ld_agent(pa + (int64_t)u * D) : 0.f;
+    }
+  }
+  float mv[kPerLane], lv[kPerLane];
+  auto load_ml = [&](int g) {
+    const float* ml = reinterpret_cast<const float*>(p.part_ml + (row0 + g) * p.splits);
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s = lane + kWave * j;
+      mv[j] = (s < nact) ? ld_agent(ml + 2 * s) : -INFINITY;
+      lv[j] = (s < nact) ? ld_agent(ml + 2 * s + 1) : 0.f;
+    }
+  };
+  if (wave < G) load_ml(wave);
+
+  for (int g = wave; g < G; g += NW) {
+    if (g != wave) load_ml(g);
+    float mloc = mv[0];
+#pragma unroll
+    for (int j = 1; j < kPerLane; ++j) mloc = fmaxf(mloc, mv[j]);
+    const float M = wave_max(mloc);
+    const float mu = (M == -INFINITY) ? 0.f : M;
+    float lloc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      mv[j] = fast_exp2(mv[j] - mu);  // 0 for the padding (-inf)
+      lloc = fmaf(mv[j], lv[j], lloc);
+    }
+    const float L = wave_sum(lloc);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) s_w[g][lane + kWave * j] = mv[j] * inv;
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int k = 0; k < kOut; ++k) {
+    const int o = tid + k * NT;
+    if (o >= G * D) continue;
+    const int g = o / D, d = o % D;
+    const float* pa = p.part_acc + (row0 + g) * p.splits * D + d;
+    float a = 0.f;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][u], t[k][u], a);
+    for (int s0 = kBatch; s0 < nact; s0 += kBatch) {
+      float x[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) x[u] = (s0 + u < nact) ? ld_agent(pa + (int64_t)(s0 + u) * D) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][s0 + u], x[u], a);
+    }
+    p.out[(int64_t)b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
+  }
+}
+
+// One tile of KV rows held in VGPRs: position pos0 + ROWS * i for i < PPT (pos0 = tile start + this lane's row).
+template <int PPT>
+struct Tile {
+  uint4 k[PPT], v[PPT];
+  float m[PPT];
+};
+
+// Issue every K and V load of a tile (and its mask values) before any arithmetic. Positions >= hi are not read.
+template <int ROWS, int PPT, int MK>
+__device__ __forceinline__ void load_tile(Tile<PPT>& t, const uint16_t* kb, const uint16_t* vb, int64_t ss,
+                                          const void* mask, int64_t mrow, int pos0, int hi) {
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int pos = pos0 + ROWS * i;
+    if (pos < hi) {
+      t.k[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)pos * ss);
+      t.v[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)pos * ss);
+    } else {
+      t.k[i] = make_uint4(0, 0, 0, 0);
+      t.v[i] = make_uint4(0, 0, 0, 0);
+    }
+    if (MK != BZ_MASK_NONE) t.m[i] = (pos < hi) ? load_mask<MK>(mask, mrow + pos) : 0.f;
+  }
+}
+
+// Fold one tile into the running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP row sum,
+// scaled by scale * log2(e); online softmax in base 2 with one max per wave (m is wave-uniform, l and acc per row);
+// then P.V in fp32 on the unpacked V registers.
+// A slot whose row lies past hi is skipped (the condition is uniform over the row's lanes, so the DPP sum, which
+// reads only lanes of the same row, never sees a skipped lane).
+// Fused prologue: the slot newpos (>= 0 only in the workgroup whose chunk holds it) takes the new k / v computed in
+// registers; the cache write of this call is not read back.
+template <int LPR, int ROWS, int G, int PPT, int MK, bool FUSED>
+__device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G], float scale_log2, float (&m)[G],
+                                             float (&l)[G], float (&acc)[G][8], int pos0, int hi, int newpos,
+                                             const uint4& knew, const uint4& vnew) {
+  float s[G][PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[g][i] = -INFINITY;
+    const int pos = pos0 + ROWS * i;
+    if (pos < hi) {
+      if (FUSED && pos == newpos) {
+        t.k[i] = knew;
+        t.v[i] = vnew;
+      }
+      bool inc = true;
+      if (MK != BZ_MASK_NONE) {
+        inc = t.m[i] > kExcluded;
+        // an excluded position must not touch the accumulator even through 0 * V (V may hold NaN there)
+        if (!inc) t.v[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = dot2_bf16(qp[g].x, t.k[i].x, 0.f);
+        d = dot2_bf16(qp[g].y, t.k[i].y, d);
+        d = dot2_bf16(qp[g].z, t.k[i].z, d);
+        d = dot2_bf16(qp[g].w, t.k[i].w, d);
+        d = row_sum<LPR>(d) * scale_log2;
+        if (MK != BZ_MASK_NONE) d = fmaf(t.m[i], kLog2e, d);
+        if (inc) s[g][i] = d;
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mt = s[g][0];
+#pragma unroll
+    for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
+    // one running max per wave: the rows of a wave can then be merged by plain sums
+    if (LPR == 8) mt = fmaxf(mt, lane_xor<8>(mt));
+    mt = fmaxf(mt, lane_xor<16>(mt));
+    mt = fmaxf(mt, lane_xor<32>(mt));
+    const float mn = fmaxf(m[g], mt);
+    const float mu = (mn == -INFINITY) ? 0.f : mn;
+    const float alpha = fast_exp2(m[g] - mu);
+    l[g] *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      s[g][i] = fast_exp2(s[g][i] - mu);
+      l[g] += s[g][i];
+    }
+    m[g] = mn;
+  }
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    if (pos0 + ROWS * i < hi) {
+      float vf[8];
+      unpack8(t.v[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
+    }
+  }
+}
+
+// Add lane (lane ^ OFF)'s (l, acc), which covers the same dims for other KV rows under the same wave-uniform max.
+// Both lanes end with the same sums.
+template <int OFF, int G>
+__device__ __forceinline__ void sum_rows(float (&l)[G], float (&acc)[G][8]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] += lane_xor<OFF>(l[g]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] += lane_xor<OFF>(acc[g][j]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- kernels
+
+template <int D, int G, int PPT, int MK, int NT, bool FUSED>
+__global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
+  constexpr int NW = NT / kWave;        // waves per workgroup
+  constexpr int LPR = D / 8;            // lanes per KV row, 16 B (8 bf16) each
+  constexpr int ROWS = NT / LPR;        // KV rows per load instruction across the workgroup
+  constexpr int TP = ROWS * PPT;        // positions per tile
+  constexpr int RPW = kWave / LPR;      // rows per wave
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
+
+  // q of the G heads of this group, this lane's 8 dims (fused: raw q, new k, new v, norm weights and RoPE tables):
+  // issued first, since none of it depends on the row's length
+  uint16_t qh[G][8];
+  uint4 xq[G], xk, xv, wq, wk, rc, rs;
+  int64_t newpos64 = -1;
+  if (FUSED) {
+    const uint16_t* row = p.qkv + (int64_t)b * p.qkv_sb + 8 * c;
+#pragma unroll
+    for (int g = 0; g < G; ++g) xq[g] = *reinterpret_cast<const uint4*>(row + (int64_t)(h * G + g) * D);
+    xk = *reinterpret_cast<const uint4*>(row + (int64_t)(p.NH + h) * D);
+    xv = *reinterpret_cast<const uint4*>(row + (int64_t)(p.NH + p.NKV + h) * D);
+    wq = *reinterpret_cast<const uint4*>(p.qn_w + 8 * c);
+    wk = *reinterpret_cast<const uint4*>(p.kn_w + 8 * c);
+    rc = *reinterpret_cast<const uint4*>(p.cos + (int64_t)b * p.cs_sb + 8 * c);
+    rs = *reinterpret_cast<const uint4*>(p.sin + (int64_t)b * p.cs_sb + 8 * c);
+    newpos64 = p.cache_pos[0];
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint16_t* qsrc = p.q + (int64_t)b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + 8 * c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qh[g][j] = qsrc[j];
+    }
+  }
+
+  int start, end;
+  row_range(p, b, start, end);
+  const int len = end - start;
+  const int chunk = split_chunk(len, p.splits, p.min_chunk);
+  const int nact = split_count(len, chunk);
+  if (split >= nact) return;
+  const int lo = start + split * chunk;
+  const int hi = min(lo + chunk, end);
+
+  const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + 8 * c;
+  const uint16_t* kb = p.k + head_off;
+  const uint16_t* vb = p.v + head_off;
+  const int64_t mrow = (int64_t)b * p.m_sb;
+
+  // The first tile's K/V loads (and, for PPT <= 4, the second's) go out before q is converted, so no wave waits on
+  // q before streaming. Tiles A and B ping-pong without register copies: while one is consumed the other's loads
+  // are in flight. Loads of positions >= hi are skipped, so a one-tile chunk issues no extra traffic.
+  constexpr bool kPingPong = PPT <= 4;
+  Tile<PPT> ta, tb;
+  load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, lo + r, hi);
+  if (kPingPong) load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, lo + TP + r, hi);
+
+  uint4 qp[G], knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
+  int newpos = -1;
+  if (FUSED) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) qp[g] = norm_rope8<LPR>(xq[g], wq, rc, rs, p.eps, c);
+    knew = norm_rope8<LPR>(xk, wk, rc, rs, p.eps, c);
+    vnew = xv;
+    if (newpos64 >= 0 && newpos64 < p.cap) {
+      const int pos = (int)newpos64;
+      // one writer per (row, kv head): the workgroup whose chunk holds the slot, or split 0 when the slot lies
+      // outside the row's attended range; only that workgroup can read the slot in this call, from registers
+      const bool in_range = pos >= start && pos < end;
+      const bool owner = in_range ? (pos >= lo && pos < hi) : (split == 0);
+      if (owner) {
+        if (in_range) newpos = pos;
+        if (tid < LPR) {
+          const int64_t off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + (int64_t)pos * p.kv_ss + 8 * c;
+          *reinterpret_cast<uint4*>(p.k_out + off) = knew;
+          *reinterpret_cast<uint4*>(p.v_out + off) = vnew;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      qp[g].x = qh[g][0] | ((uint32_t)qh[g][1] << 16);
+      qp[g].y = qh[g][2] | ((uint32_t)qh[g][3] << 16);
+      qp[g].z = qh[g][4] | ((uint32_t)qh[g][5] << 16);
+      qp[g].w = qh[g][6] | ((uint32_t)qh[g][7] << 16);
+    }
+  }
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
+  }
+
+  if (kPingPong) {
+    for (int t0 = lo; t0 < hi; t0 += 2 * TP) {
+      consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
+      if (t0 + TP >= hi) break;
+      load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + 2 * TP + r, hi);
+      consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(tb, qp, p.scale_log2, m, l, acc, t0 + TP + r, hi, newpos, knew, vnew);
+      load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, t0 + 3 * TP + r, hi);
+    }
+  } else {
+    for (int t0 = lo; t0 < hi; t0 += TP) {
+      consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
+      if (t0 + TP < hi) load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + TP + r, hi);
+    }
+  }
+
+  // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims)
+  if (LPR == 8) sum_rows<8, G>(l, acc);
+  sum_rows<16, G>(l, acc);
+  sum_rows<32, G>(l, acc);
+
+  // merge the NW waves through LDS
+  __shared__ float s_acc[NW][G][D];
+  __shared__ float s_m[NW][G], s_l[NW][G];
+  const int w = tid / kWave, lane = tid % kWave;
+  if (lane < LPR) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_acc[w][g][8 * c + j] = acc[g][j];
+      if (lane == 0) {
+        s_m[w][g] = m[g];
+        s_l[w][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  (void)RPW;
+
+  for (int o = tid; o < G * D; o += NT) {
+    const int g = o / D, d = o % D, hq = h * G + g;
+    float M = s_m[0][g];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) M = fmaxf(M, s_m[u][g]);
+    const float mu = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float e = fast_exp2(s_m[u][g] - mu);
+      L = fmaf(e, s_l[u][g], L);
+      A = fmaf(e, s_acc[u][g][d], A);
+    }
+    if (nact == 1) {
+      p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(L > 0.f ? A / L : 0.f);
+    } else {
+      const int64_t ps = ((int64_t)b * p.NH + hq) * p.splits + split;
+      st_agent(p.part_acc + ps * D + d, A);
+      if (d == 0) {
+        st_agent(reinterpret_cast<float*>(p.part_ml + ps), M);
+        st_agent(reinterpret_cast<float*>(p.part_ml + ps) + 1, L);
+      }
+    }
+  }
+  if (nact == 1 || !p.combine_last) return;
+
+  // Last-arriving workgroup of this (b, kv head) merges the splits. Each wave waits until its agent-scope partial
+  // stores have completed (s_waitcnt vmcnt(0); gfx9 encoding with expcnt/lgkmcnt left open), the barrier collects
+  // the waves, and thread 0 counts the workgroup in with one agent-scope RMW. The workgroup that brings the
+  // count to nact reads the partials with agent-scope loads; it resets the counter for the next call.
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  __syncthreads();
+  if (tid == 0) {
+    int* cnt = p.counters + (b * p.NKV + h) * kCounterStride;
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == nact - 1);
+    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  merge_splits<D, G, NT>(p, b, h, nact);
+}
+
+// Second-launch merge: one workgroup per (kv head, row).
+template <int D, int G>
+__global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  int start, end;
+  row_range(p, b, start, end);
+  const int len = end - start;
+  const int nact = split_count(len, split_chunk(len, p.splits, p.min_chunk));
+  if (nact == 1) return;  // the split kernel wrote the output
+  merge_splits<D, G, kThreads>(p, b, h, nact);
+}
+
+// Interval of the additive mask row: first and last position with value > -1e30.
+template <int MK>
+__global__ void __launch_bounds__(kThreads) mask_range_kernel(const void* mask, int64_t m_sb, int cap,
+                                                              int32_t* start, int32_t* end) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  int lo = cap, hi = -1;
+  for (int pos = tid; pos < cap; pos += kThreads) {
+    if (load_mask<MK>(mask, (int64_t)b * m_sb + pos) > kExcluded) {
+      lo = min(lo, pos);
+      hi = max(hi, pos);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    lo = min(lo, __shfl_xor(lo, off));
+    hi = max(hi, __shfl_xor(hi, off));
+  }
+  __shared__ int s_lo[kWaves], s_hi[kWaves];
+  if (tid % kWave == 0) {
+    s_lo[tid / kWave] = lo;
+    s_hi[tid / kWave] = hi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int u = 1; u < kWaves; ++u) {
+      lo = min(lo, s_lo[u]);
+      hi = max(hi, s_hi[u]);
+    }
+    const bool any = hi >= 0;
+    start[b] = any ? lo : 0;
+    end[b] = any ? hi + 1 : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- kernel tables
+
+template <int D, int G, int MK, int NT, bool FUSED>
+SplitFn pick_ppt(int ppt) {
+  switch (ppt) {
+    case 1: return gqa_split_kernel<D, G, 1, MK, NT, FUSED>;
+    case 2: return gqa_split_kernel<D, G, 2, MK, NT, FUSED>;
+    default: return gqa_split_kernel<D, G, 4, MK, NT, FUSED>;
+  }
+}
+
+template <int D, int G, int NT, bool FUSED>
+SplitFn pick_mask(int mk, int ppt) {
+  switch (mk) {
+    case BZ_MASK_BF16: return pick_ppt<D, G, BZ_MASK_BF16, NT, FUSED>(ppt);
+    case BZ_MASK_F32: return pick_ppt<D, G, BZ_MASK_F32, NT, FUSED>(ppt);
+    default: return pick_ppt<D, G, BZ_MASK_NONE, NT, FUSED>(ppt);
+  }
+}
+
+template <int D, int NT, bool FUSED>
+SplitFn pick_group(int G, int mk, int ppt) {
+  switch (G) {
+    case 1: return pick_mask<D, 1, NT, FUSED>(mk, ppt);
+    case 2: return pick_mask<D, 2, NT, FUSED>(mk, ppt);
+    case 4: return pick_mask<D, 4, NT, FUSED>(mk, ppt);
+    case 8: return pick_mask<D, 8, NT, FUSED>(mk, ppt);
+    default: return nullptr;
+  }
+}
+
+}  // namespace

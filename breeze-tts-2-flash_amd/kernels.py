@@ -11,7 +11,9 @@ import ctypes
 import os
 import shutil
 import subprocess
+import tempfile
 import threading
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -20,19 +22,20 @@ REPO_DIR = PKG_DIR.parent
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libbz_gqa_decode.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["gqa_decode.hip"]
+SOURCES = ["gqa_decode.hip", "gqa_fused.hip"]  # translation units, compiled in parallel
+HEADERS = ["gqa_kernels.cuh"]
 ARCH = "gfx950"
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32)
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
-    "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_workspace_size", "bz_gqa_decode_default_splits",
-    "bz_status_string", "bz_gqa_decode_abi_version",
+    "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_fused", "bz_gqa_decode_workspace_size",
+    "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version",
 )
 
 MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
@@ -56,6 +59,17 @@ class GqaDecodeArgs(ctypes.Structure):
     ]
 
 
+class GqaDecodeFusedArgs(ctypes.Structure):
+    """Mirror of struct bz_gqa_decode_fused_args."""
+    _fields_ = [
+        ("base", GqaDecodeArgs),
+        ("qkv", ctypes.c_void_p), ("qkv_stride_b", ctypes.c_int64),
+        ("q_norm_weight", ctypes.c_void_p), ("k_norm_weight", ctypes.c_void_p), ("eps", ctypes.c_float),
+        ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("rope_stride_b", ctypes.c_int64),
+        ("cache_pos", ctypes.c_void_p),
+    ]
+
+
 _LOCK = threading.Lock()
 _LIB = None
 
@@ -67,19 +81,37 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libbz_gqa_decode.so)")
 
 
-def build_command(out: Path = LIB_PATH) -> list[str]:
-    return [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", str(out), *[str(CSRC / s) for s in SOURCES]]
+def compile_commands(objdir: Path) -> list[list[str]]:
+    """One hipcc -c command per translation unit (objects into objdir)."""
+    return [[hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o",
+             str(objdir / (Path(src).stem + ".o"))] for src in SOURCES]
+
+
+def link_command(objdir: Path, out: Path) -> list[str]:
+    return [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(out),
+            *[str(objdir / (Path(src).stem + ".o")) for src in SOURCES]]
 
 
 def build(verbose: bool = False) -> Path:
     """Compile libbz_gqa_decode.so for gfx950 in-tree (always recompiles). Returns its path."""
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = build_command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+    with tempfile.TemporaryDirectory(prefix="bz_gqa_build_") as d:
+        objdir = Path(d)
+        cmds = compile_commands(objdir)
+
+        def run(cmd):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            return subprocess.run(cmd, capture_output=True, text=True)
+
+        with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+            results = list(pool.map(run, cmds))
+        for cmd, res in zip(cmds, results):
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc failed ({res.returncode}) on {cmd[-3]}:\n{res.stderr[-4000:]}")
+        res = run(link_command(objdir, tmp))
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{res.stderr[-4000:]}")
     os.replace(tmp, LIB_PATH)  # atomic: a concurrent load() sees the old or the new library, never half of one
     return LIB_PATH
 
@@ -90,6 +122,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_gqa_decode.restype = ctypes.c_int
     lib.bz_gqa_decode_masked.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p]
     lib.bz_gqa_decode_masked.restype = ctypes.c_int
+    lib.bz_gqa_decode_fused.argtypes = [P(GqaDecodeFusedArgs), ctypes.c_void_p]
+    lib.bz_gqa_decode_fused.restype = ctypes.c_int
     lib.bz_gqa_decode_workspace_size.argtypes = [ctypes.c_int32] * 7 + [P(ctypes.c_size_t)]
     lib.bz_gqa_decode_workspace_size.restype = ctypes.c_int
     lib.bz_gqa_decode_default_splits.argtypes = [ctypes.c_int32] * 5 + [P(ctypes.c_int32)]

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 1
+#define BZ_GQA_DECODE_ABI_VERSION 2
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -113,6 +113,31 @@ int bz_gqa_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t he
    bz_gqa_decode with that mask applied inside the interval. args->seq_lens / args->kv_start are ignored; args->mask
    is required. Replaces attn_decode's mask argument (bb_attn.cu:416-418, mask scan :111-117). */
 int bz_gqa_decode_masked(const bz_gqa_decode_args* args, hipStream_t stream);
+
+/* Arguments of bz_gqa_decode_fused: the raw q | k | v projections of the decode token, the q / k RMSNorm weights and
+   the RoPE tables, and the cache slot the new k and v go to. base.q is ignored (q comes from qkv); base.k_cache and
+   base.v_cache must be writable; head_dim must be 128. All pointers and strides 16-byte aligned. */
+typedef struct bz_gqa_decode_fused_args {
+  bz_gqa_decode_args base;
+  /* [batch, (num_q_heads + 2 * num_kv_heads) * head_dim] bf16: q heads, then k heads, then v heads (Qwen3 q/k/v_proj) */
+  const void* qkv;
+  int64_t qkv_stride_b;
+  const void* q_norm_weight;  /* [head_dim] bf16 */
+  const void* k_norm_weight;  /* [head_dim] bf16 */
+  float eps;                  /* RMSNorm epsilon */
+  const void* cos;            /* [batch, head_dim] bf16 RoPE tables of this token's position */
+  const void* sin;
+  int64_t rope_stride_b;
+  const int64_t* cache_pos;   /* device scalar: the cache slot written with the new k and v (all rows) */
+} bz_gqa_decode_fused_args;
+
+/* Fused decode step: q_norm / k_norm (Qwen3 RMSNorm) and RoPE on the raw projections at the eager bf16 rounding points,
+   the new k (normed, roped) and v written into slot *cache_pos of every row's cache (skipped when the slot lies
+   outside [0, capacity)), then bz_gqa_decode over the updated cache. With base.seq_lens set, rows attend
+   [kv_start, seq_lens); with base.seq_lens NULL, the range comes from base.mask as in bz_gqa_decode_masked.
+   Replaces attn_decode_fused (flash/csrc/bb_attn.cu:433-460, prologue :78-149, pybind :466-469), the entry the
+   reference's decode step calls (flash/backbone.py:123-124). */
+int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* args, hipStream_t stream);
 
 /* Human-readable text of a bz_status. */
 const char* bz_status_string(int status);

@@ -137,3 +137,64 @@ def mask_interval(mask) -> tuple[np.ndarray, np.ndarray]:
         if idx.size:
             start[b], end[b] = idx[0], idx[-1] + 1
     return start, end
+
+
+# ---------------------------------------------------------------------------------------------- fused prologue
+
+def qk_norm_rope(x_bits, w_bits, eps: float, cos_bits, sin_bits):
+    """Qwen3 per-head RMSNorm then RoPE, at the eager bf16 rounding points (flash/csrc/bb_attn.cu:78-100, which
+    reproduces transformers' Qwen3RMSNorm + apply_rotary_pos_emb, models/breeze.py:211-242):
+        h = bf16(x * rsqrt(mean(x^2) + eps))          (x, mean, rsqrt in fp32)
+        y = bf16(w * h)
+        out = bf16(bf16(y * cos) + bf16(rotate_half(y) * sin)),  rotate_half(y) = [-y[D/2:], y[:D/2]]
+    x_bits [..., D], w/cos/sin bits broadcastable to it, all bf16 bit patterns (uint16). Returns uint16 bits."""
+    from .bf16 import bf16_to_f32, f32_to_bf16, round_to_bf16
+
+    x = bf16_to_f32(x_bits).astype(np.float32)
+    w = bf16_to_f32(w_bits).astype(np.float32)
+    cos = bf16_to_f32(cos_bits).astype(np.float32)
+    sin = bf16_to_f32(sin_bits).astype(np.float32)
+    var = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt(var + np.float32(eps), dtype=np.float32)).astype(np.float32)
+    h = round_to_bf16((x * r).astype(np.float32))
+    y = round_to_bf16((w * h).astype(np.float32))
+    half = y.shape[-1] // 2
+    rot = np.concatenate([-y[..., half:], y[..., :half]], axis=-1)
+    a = round_to_bf16((y * cos).astype(np.float32))
+    b = round_to_bf16((rot * sin).astype(np.float32))
+    return f32_to_bf16((a + b).astype(np.float32))
+
+
+def fused_decode(qkv_bits, qn_w_bits, kn_w_bits, eps: float, cos_bits, sin_bits, k_bits, v_bits, cache_pos: int,
+                 seq_lens, scale: float, kv_start=None, mask=None):
+    """Restatement of attn_decode_fused (bb_attn.cu:433-460, prologue :118-149): split the raw projections
+    qkv [B, (NH + 2 NKV) * D] into q | k | v heads, apply q_norm / k_norm + RoPE (qk_norm_rope, cos/sin [B, D]),
+    write the new k (normed, roped) and v (raw) into cache slot cache_pos of every row (when 0 <= cache_pos <
+    capacity), then attend with decode_attention over the updated cache. Bits are bf16 patterns (uint16).
+    Returns (out float64 [B, NH, D], k_bits, v_bits) with the updated caches (copies)."""
+    from .bf16 import bf16_to_f32
+
+    B, NKV, cap, D = k_bits.shape
+    NH = qkv_bits.shape[1] // D - 2 * NKV
+    heads = qkv_bits.reshape(B, NH + 2 * NKV, D)
+    cs, sn = cos_bits.reshape(B, 1, D), sin_bits.reshape(B, 1, D)
+    q = qk_norm_rope(heads[:, :NH], qn_w_bits, eps, cs, sn)
+    k_new = qk_norm_rope(heads[:, NH:NH + NKV], kn_w_bits, eps, cs, sn)
+    v_new = heads[:, NH + NKV:]
+    k_bits, v_bits = k_bits.copy(), v_bits.copy()
+    if 0 <= cache_pos < cap:
+        k_bits[:, :, cache_pos] = k_new
+        v_bits[:, :, cache_pos] = v_new
+    out = decode_attention(bf16_to_f32(q), bf16_to_f32(k_bits), bf16_to_f32(v_bits), seq_lens, scale,
+                           kv_start=kv_start, mask=mask)
+    return out, k_bits, v_bits
+
+
+def rope_cos_sin(positions, head_dim: int, base: float = 1_000_000.0):
+    """Standard RoPE tables for the given positions (the Qwen3 default rope_theta is 1e6): cos/sin [n, head_dim]
+    float32 with inv_freq = base^(-2i/D) repeated over both halves, as transformers' rotary embedding builds them."""
+    pos = np.asarray(positions, dtype=np.float64)[:, None]
+    inv = base ** (-np.arange(0, head_dim, 2, dtype=np.float64) / head_dim)
+    ang = pos * inv[None, :]
+    emb = np.concatenate([ang, ang], axis=-1)
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)

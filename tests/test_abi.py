@@ -67,6 +67,24 @@ def test_struct_layout_matches_c(K, tmp_path):
         assert int(got[f]) == getattr(K.GqaDecodeArgs, f).offset, f
 
 
+def test_fused_struct_layout_matches_c(K, tmp_path):
+    fields = [f for f, _ in K.GqaDecodeFusedArgs._fields_]
+    src = ["#include <stddef.h>", "#include <stdio.h>", '#include "bz_gqa_decode.h"', "int main(void) {",
+           '  printf("size %zu\\n", sizeof(bz_gqa_decode_fused_args));']
+    src += [f'  printf("{f} %zu\\n", offsetof(bz_gqa_decode_fused_args, {f}));' for f in fields]
+    src += ["  return 0;", "}"]
+    c = tmp_path / "layout_fused.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout_fused"
+    subprocess.run(["gcc", "-std=c11", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{REPO / 'include'}",
+                    str(c), "-o", str(exe)], check=True)
+    got = dict(ln.split() for ln in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                   check=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(K.GqaDecodeFusedArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(K.GqaDecodeFusedArgs, f).offset, f
+
+
 def test_status_strings(lib):
     for code in range(0, -10, -1):
         s = lib.bz_status_string(code).decode()
@@ -136,3 +154,33 @@ def test_workspace_size(lib):
     assert _ws(lib, 2, 16, 8, 96, 2048, 4, 0)[0] == -3
     assert _ws(lib, 2, 16, 8, 128, 2048, 300, 0)[0] == -2
     assert lib.bz_gqa_decode_workspace_size(2, 16, 8, 128, 2048, 4, 0, None) == -1
+
+
+def _good_fused(K, **over):
+    f = K.GqaDecodeFusedArgs()
+    f.base = _good_args(K, q=None, workspace=None)
+    f.qkv, f.qkv_stride_b = 0x70000, (16 + 2 * 8) * 128
+    f.q_norm_weight, f.k_norm_weight, f.eps = 0x71000, 0x72000, 1e-6
+    f.cos, f.sin, f.rope_stride_b = 0x73000, 0x74000, 128
+    f.cache_pos = 0x75000
+    for k, v in over.items():
+        if k.startswith("base_"):
+            setattr(f.base, k[5:], v)
+        else:
+            setattr(f, k, v)
+    return f
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(qkv=None), -1), (dict(q_norm_weight=None), -1), (dict(cos=None), -1), (dict(cache_pos=None), -1),
+    (dict(base_head_dim=64, base_kv_stride_s=64, base_kv_stride_h=256 * 64, base_kv_stride_b=8 * 256 * 64), -3),
+    (dict(qkv_stride_b=100), -2), (dict(rope_stride_b=64), -2),
+    (dict(qkv=0x70008), -4), (dict(cos=0x73004), -4), (dict(qkv_stride_b=32 * 128 + 4), -4),
+    (dict(cache_pos=0x75004), -4),
+    (dict(), -5),                                             # no workspace (checked before any launch)
+    (dict(base_seq_lens=None), -1),                           # interval form needs a mask
+])
+def test_fused_validation(lib, K, over, code):
+    f = _good_fused(K, **over)
+    assert lib.bz_gqa_decode_fused(ctypes.byref(f), None) == code
+    assert lib.bz_gqa_decode_fused(None, None) == -1
