@@ -104,6 +104,59 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold):
     return us, read_bytes, nsets
 
 
+def time_fused(pkg, w, dev, steps, warmup, splits):
+    """µs per fused decode step (bz_gqa_decode_fused) on workload w: the token at slot seq_len - 1 is normed, roped,
+    written into the cache and attended, as the reference's decode step calls attn_decode_fused. Cold rotation over
+    K/V sets as in time_calls (every call rewrites the same slot of its set with the same values)."""
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    g = w.to(dev)
+    B, NH, NKV, D = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim
+    L = int(w.seq_lens[0])
+    if any(int(x) != L for x in w.seq_lens):
+        raise ValueError("time_fused needs one length for every row")
+    gen = torch.Generator().manual_seed(100 + L)
+    qkv = (torch.randn(B, (NH + 2 * NKV) * D, generator=gen) * 3).to(torch.bfloat16).to(dev)
+    qn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(dev)
+    kn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(dev)
+    inv = 1e6 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = torch.cat([(L - 1) * inv] * 2)
+    cos = ang.cos().to(torch.bfloat16).expand(B, D).contiguous().to(dev)
+    sin = ang.sin().to(torch.bfloat16).expand(B, D).contiguous().to(dev)
+    cache_pos = torch.tensor([L - 1], dtype=torch.int64, device=dev)
+    nbytes = workloads.fused_algorithmic_bytes(w.seq_lens.tolist(), NH, NKV, D)
+    nsets = min(steps, max(16, math.ceil(640e6 / nbytes)))
+    ks = torch.empty((nsets,) + tuple(g.k.shape), dtype=g.k.dtype, device=dev)
+    vs = torch.empty_like(ks)
+    ks.copy_(g.k.expand_as(ks))
+    vs.copy_(g.v.expand_as(vs))
+    out = torch.empty(B, NH, D, dtype=torch.bfloat16, device=dev)
+
+    def call(i):
+        pkg.gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, ks[i % nsets], vs[i % nsets], cache_pos, g.scale, out,
+                             seq_lens=g.seq_lens, num_splits=splits)
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            call(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / steps
+    del ks, vs
+    return us, nbytes, nsets
+
+
 def time_depth_frame(pkg, dev, steps, warmup):
     """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph."""
     import torch
@@ -264,6 +317,13 @@ def main():
             print(f"[bench] config {xc} cold: {us_c:.3f} us/call, {nb / us_c / 1e3:.1f} GB/s", file=sys.stderr,
                   flush=True)
             del w
+        if w2.head_dim == 128 and len(set(w2.seq_lens.tolist())) == 1:
+            us_x, nbx, nsx = time_fused(pkg, w2, dev, args.steps, args.warmup, args.splits)
+            extra[f"config{cfg}_fused_cold"] = {
+                "entry": "bz_gqa_decode_fused (q/k RMSNorm + RoPE + cache-slot write + attention)",
+                "us_per_call": round(us_x, 3), "GB/s": round(nbx / us_x / 1e3, 1),
+                "pct_of_peak_hbm": round(100.0 * nbx / us_x / 1e3 / PEAK_HBM_GBS, 1), "bytes": nbx, "sets": nsx}
+            print(f"[bench] config {cfg} fused cold: {us_x:.3f} us/call", file=sys.stderr, flush=True)
         us_f, fb = time_depth_frame(pkg, dev, args.steps, args.warmup)
         extra["config5_depth_frame"] = {"us_per_frame": round(us_f, 3), "us_per_call": round(us_f / 32, 3),
                                         "bytes_per_frame": fb, "GB/s": round(fb / us_f / 1e3, 1)}

@@ -228,6 +228,9 @@ int check_common(const bz_gqa_decode_args* a, bool need_q) {
   if ((kp | vp) & 15) return BZ_ERR_ALIGNMENT;
   if ((a->kv_stride_b | a->kv_stride_h | a->kv_stride_s) & 7) return BZ_ERR_ALIGNMENT;
   if (a->kv_stride_s < a->head_dim) return BZ_ERR_SHAPE;
+  // K/V are read through buffer resources with 32-bit byte offsets per (row, kv head): every offset the kernel forms
+  // (positions below capacity + 1024, the largest read-ahead) must stay below 2^31
+  if (((int64_t)a->capacity + 1024) * a->kv_stride_s * 2 > INT32_MAX) return BZ_ERR_SHAPE;
   if (a->mask_dtype < BZ_MASK_NONE || a->mask_dtype > BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
   return BZ_OK;
 }

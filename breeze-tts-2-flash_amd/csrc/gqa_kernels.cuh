@@ -94,13 +94,12 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// fp32 -> bf16, round to nearest even; NaN stays NaN (quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16, round to nearest even, NaN stays NaN (quiet): gfx950's v_cvt_pk_bf16_f32, one instruction for a pair,
+// no branch.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ void unpack8(const uint4& w, float f[8]) {
   f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
@@ -159,7 +158,8 @@ __device__ __forceinline__ float lane_xor(float x) {
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
 // Value of the lane holding the same 8 dims +/- head_dim / 2 (rotate_half's partner): LPR / 2 lanes away inside the
@@ -337,21 +337,37 @@ struct Tile {
   float m[PPT];
 };
 
-// Issue every K and V load of a tile (and its mask values) before any arithmetic. Positions >= hi are not read.
+// Raw buffer resource (gfx9 V#: base, stride 0, num_records bytes, word 3 = DATA_FORMAT 32) over the bytes [0, bytes)
+// of one (row, kv head) span. A buffer load at an offset >= bytes returns zero and makes no memory access.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ Rsrc span_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRsrcWord3);
+}
+
+// The K, V (and mask) spans of one (row, kv head), each cut at position hi: positions >= hi are outside the resource,
+// so their loads return zero without reading memory (NaN tails and slots past the row stay unread).
+struct Spans {
+  Rsrc k, v, m;
+  uint32_t row_bytes;  // bytes between consecutive positions of K / V
+  uint32_t lane_off;   // this lane's 16 bytes inside a row
+};
+
+// Issue every K and V load of a tile (and its mask values) before any arithmetic. The loads are unconditional (the
+// resource bounds do the cut at hi), so the compiler's vmcnt accounting stays exact and earlier loads (q, the fused
+// prologue's inputs) can be consumed while the tile is still in flight.
 template <int ROWS, int PPT, int MK>
-__device__ __forceinline__ void load_tile(Tile<PPT>& t, const uint16_t* kb, const uint16_t* vb, int64_t ss,
-                                          const void* mask, int64_t mrow, int pos0, int hi) {
+__device__ __forceinline__ void load_tile(Tile<PPT>& t, const Spans& sp, int pos0) {
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-    const int pos = pos0 + ROWS * i;
-    if (pos < hi) {
-      t.k[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)pos * ss);
-      t.v[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)pos * ss);
-    } else {
-      t.k[i] = make_uint4(0, 0, 0, 0);
-      t.v[i] = make_uint4(0, 0, 0, 0);
-    }
-    if (MK != BZ_MASK_NONE) t.m[i] = (pos < hi) ? load_mask<MK>(mask, mrow + pos) : 0.f;
+    const uint32_t pos = (uint32_t)(pos0 + ROWS * i);
+    const uint32_t off = pos * sp.row_bytes + sp.lane_off;
+    t.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sp.k, off, 0, 0));
+    t.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sp.v, off, 0, 0));
+    if (MK == BZ_MASK_BF16) t.m[i] = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(sp.m, pos * 2, 0, 0));
+    if (MK == BZ_MASK_F32)
+      t.m[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sp.m, pos * 4, 0, 0));
   }
 }
 
@@ -490,18 +506,29 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   const int lo = start + split * chunk;
   const int hi = min(lo + chunk, end);
 
-  const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh + 8 * c;
-  const uint16_t* kb = p.k + head_off;
-  const uint16_t* vb = p.v + head_off;
-  const int64_t mrow = (int64_t)b * p.m_sb;
+  Spans sp;
+  {
+    const int64_t head_off = (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh;
+    sp.row_bytes = (uint32_t)p.kv_ss * 2;
+    sp.lane_off = 16 * c;
+    const int span = hi * (int)sp.row_bytes;  // < 2^31: the host bounds (capacity + 1024) * kv_stride_s * 2
+    sp.k = span_rsrc(p.k + head_off, span);
+    sp.v = span_rsrc(p.v + head_off, span);
+    if (MK == BZ_MASK_BF16) sp.m = span_rsrc(static_cast<const uint16_t*>(p.mask) + (int64_t)b * p.m_sb, 2 * hi);
+    if (MK == BZ_MASK_F32) sp.m = span_rsrc(static_cast<const float*>(p.mask) + (int64_t)b * p.m_sb, 4 * hi);
+  }
 
   // The first tile's K/V loads (and, for PPT <= 4, the second's) go out before q is converted, so no wave waits on
   // q before streaming. Tiles A and B ping-pong without register copies: while one is consumed the other's loads
-  // are in flight. Loads of positions >= hi are skipped, so a one-tile chunk issues no extra traffic.
+  // are in flight. Loads of positions >= hi fall outside the spans and make no memory access, so a one-tile chunk
+  // issues no extra traffic.
   constexpr bool kPingPong = PPT <= 4;
   Tile<PPT> ta, tb;
-  load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, lo + r, hi);
-  if (kPingPong) load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, lo + TP + r, hi);
+  load_tile<ROWS, PPT, MK>(ta, sp, lo + r);
+  if (kPingPong) load_tile<ROWS, PPT, MK>(tb, sp, lo + TP + r);
+  // keep the machine scheduler from sinking the tile loads below the q / prologue arithmetic (which would make that
+  // arithmetic wait for its own inputs before any K/V load is in flight)
+  __builtin_amdgcn_sched_barrier(0);
 
   uint4 qp[G], knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
   int newpos = -1;
@@ -548,14 +575,14 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     for (int t0 = lo; t0 < hi; t0 += 2 * TP) {
       consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
       if (t0 + TP >= hi) break;
-      load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + 2 * TP + r, hi);
+      load_tile<ROWS, PPT, MK>(ta, sp, t0 + 2 * TP + r);
       consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(tb, qp, p.scale_log2, m, l, acc, t0 + TP + r, hi, newpos, knew, vnew);
-      load_tile<ROWS, PPT, MK>(tb, kb, vb, p.kv_ss, p.mask, mrow, t0 + 3 * TP + r, hi);
+      load_tile<ROWS, PPT, MK>(tb, sp, t0 + 3 * TP + r);
     }
   } else {
     for (int t0 = lo; t0 < hi; t0 += TP) {
       consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
-      if (t0 + TP < hi) load_tile<ROWS, PPT, MK>(ta, kb, vb, p.kv_ss, p.mask, mrow, t0 + TP + r, hi);
+      if (t0 + TP < hi) load_tile<ROWS, PPT, MK>(ta, sp, t0 + TP + r);
     }
   }
 

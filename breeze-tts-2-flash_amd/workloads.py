@@ -111,6 +111,15 @@ def algorithmic_bytes(batch_lens, num_q_heads: int, num_kv_heads: int, head_dim:
     return kv + 2 * B * num_q_heads * head_dim * 2 + 4 * B
 
 
+def fused_algorithmic_bytes(batch_lens, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    """HBM bytes of a fused decode step (bz_gqa_decode_fused): the attention call's bytes, plus the raw k and v
+    projections (B * 2 NKV * D * 2), both norm weights (2 * D * 2), cos and sin (2 * B * D * 2), the new k and v
+    written into the cache slot (B * 2 NKV * D * 2) and cache_pos (8). The q read is already in the attention term."""
+    B = len(list(batch_lens))
+    return (algorithmic_bytes(batch_lens, num_q_heads, num_kv_heads, head_dim) + 2 * B * 2 * num_kv_heads * head_dim * 2
+            + 2 * head_dim * 2 + 2 * B * head_dim * 2 + 8)
+
+
 def flops(batch_lens, num_q_heads: int, head_dim: int) -> int:
     """4 * NH * len * D per row (q . k and p . v, multiply-add = 2 FLOPs)."""
     return sum(4 * num_q_heads * int(L) * head_dim for L in batch_lens)

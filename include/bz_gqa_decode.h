@@ -63,7 +63,9 @@ typedef struct bz_gqa_decode_args {
   const void* q;
   int64_t q_stride_b, q_stride_h;
   /* KV cache [batch, num_kv_heads, capacity, head_dim] bf16 (transformers StaticCache layer layout). K and V
-     share strides; k_cache, v_cache and all three strides must be 16-byte aligned (multiples of 8 elements). */
+     share strides; k_cache, v_cache and all three strides must be 16-byte aligned (multiples of 8 elements).
+     One (batch, kv head) span must be addressable with 31-bit byte offsets: (capacity + 1024) * kv_stride_s * 2
+     < 2^31, else BZ_ERR_SHAPE. */
   const void* k_cache;
   const void* v_cache;
   int64_t kv_stride_b, kv_stride_h, kv_stride_s;

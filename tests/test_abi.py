@@ -118,6 +118,9 @@ def _good_args(K, **over):
     (dict(combine=3), -9),
     (dict(workspace=None), -5), (dict(workspace=0x60000, workspace_bytes=16), -5),
     (dict(workspace=0x60010, workspace_bytes=1 << 30), -4),
+    # 31-bit byte offsets inside one (row, kv head) span: (capacity + 1024) * kv_stride_s * 2 < 2^31
+    (dict(capacity=(1 << 23) - 1024, num_splits=4), -2), (dict(capacity=1 << 20, kv_stride_s=1024), -2),
+    (dict(capacity=(1 << 23) - 1025, num_splits=4), -5),   # just inside the bound: fails later, on the workspace
 ])
 def test_host_validation(lib, K, over, code):
     a = _good_args(K, **over)

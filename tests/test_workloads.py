@@ -14,6 +14,9 @@ def test_algorithmic_bytes_match_published_counts():
     frame = sum(workloads.algorithmic_bytes([L, L], 16, 8, 64) for L in range(1, 33))
     assert frame == 2_425_088
     assert workloads.flops([1024, 1024], 16, 128) == 16_777_216
+    # fused step: + raw k and v (2 rows x 2 x 8 heads x 128 x 2 B), 2 norm weights, cos/sin [2, 128], the slot write
+    # of k and v (same size as the raw reads) and the int64 cache_pos
+    assert workloads.fused_algorithmic_bytes([1024, 1024], 16, 8, 128) == 8_405_000 + 8192 + 512 + 1024 + 8192 + 8
 
 
 def test_config_shapes_and_determinism():
