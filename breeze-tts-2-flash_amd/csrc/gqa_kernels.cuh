@@ -110,8 +110,6 @@ __device__ __forceinline__ void unpack8(const uint4& w, float f[8]) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
 // c + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs, accumulated in fp32 (v_dot2c_f32_bf16)
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
@@ -155,11 +153,19 @@ __device__ __forceinline__ float lane_xor(float x) {
   }
 }
 
-__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
-
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t f = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
+// Round 8 floats to bf16 precision in place (RNE), two per conversion.
+__device__ __forceinline__ void round8(float (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const uint32_t w = pack_bf16x2(v[j], v[j + 1]);
+    v[j] = bf16_lo(w);
+    v[j + 1] = bf16_hi(w);
+  }
 }
 
 // Value of the lane holding the same 8 dims +/- head_dim / 2 (rotate_half's partner): LPR / 2 lanes away inside the
@@ -190,17 +196,30 @@ __device__ __forceinline__ uint4 norm_rope8(const uint4& xr, const uint4& wr, co
   const float inv_rms = rsqrtf(ss * (1.f / (8 * LPR)) + eps);
   float y[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) y[j] = round_bf16(w[j] * round_bf16(x[j] * inv_rms));
+  for (int j = 0; j < 8; ++j) y[j] = x[j] * inv_rms;
+  round8(y);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] *= w[j];
+  round8(y);
   const bool first_half = c < LPR / 2;
-  float o[8];
+  float yc[8], ys[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float partner = half_partner<LPR>(y[j]);
-    const float rot = first_half ? -partner : partner;
-    o[j] = round_bf16(y[j] * cs[j]) + round_bf16(rot * sn[j]);
+    yc[j] = y[j] * cs[j];
+    ys[j] = (first_half ? -partner : partner) * sn[j];
   }
-  return make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
-                    pack_bf16x2(o[6], o[7]));
+  round8(yc);
+  round8(ys);
+  return make_uint4(pack_bf16x2(yc[0] + ys[0], yc[1] + ys[1]), pack_bf16x2(yc[2] + ys[2], yc[3] + ys[3]),
+                    pack_bf16x2(yc[4] + ys[4], yc[5] + ys[5]), pack_bf16x2(yc[6] + ys[6], yc[7] + ys[7]));
+}
+
+// The four dwords of x from lane src_lane of the wave (ds_bpermute through the LDS crossbar; no LDS storage).
+__device__ __forceinline__ uint4 lane_fetch4(const uint4& x, int src_lane) {
+  const int a = src_lane * 4;
+  return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)x.x), (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)x.y),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)x.z), (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)x.w));
 }
 
 // Clamp the row's range so that no access can leave [0, capacity).
@@ -472,19 +491,27 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
 
-  // q of the G heads of this group, this lane's 8 dims (fused: raw q, new k, new v, norm weights and RoPE tables):
-  // issued first, since none of it depends on the row's length
+  // q of the G heads of this group, this lane's 8 dims, issued first, since none of it depends on the row's length.
+  // Fused: the prologue's inputs instead. Its NE = G + 1 heads (the G q heads, then the new k) are spread over the
+  // RPW rows of each wave, head e on row e % RPW (slot e / RPW), so a row normalises and rotates NS heads rather than
+  // all NE; the results are then fetched across rows.
+  constexpr int NE = G + 1;
+  constexpr int NS = (NE + RPW - 1) / RPW;
+  static_assert(!FUSED || D == 128, "the fused prologue is built for head_dim 128");
+  const int rw = (tid % kWave) / LPR;  // row inside the wave
   uint16_t qh[G][8];
-  uint4 xq[G], xk, xv, wq, wk, rc, rs;
+  uint4 xe[NS], we[NS], xv, rc, rs;
   int64_t newpos64 = -1;
   if (FUSED) {
     const uint16_t* row = p.qkv + (int64_t)b * p.qkv_sb + 8 * c;
 #pragma unroll
-    for (int g = 0; g < G; ++g) xq[g] = *reinterpret_cast<const uint4*>(row + (int64_t)(h * G + g) * D);
-    xk = *reinterpret_cast<const uint4*>(row + (int64_t)(p.NH + h) * D);
+    for (int s = 0; s < NS; ++s) {
+      const int e = min(s * RPW + rw, G);  // rows past the last head redo the k head (result unused)
+      const int64_t col = e < G ? (int64_t)(h * G + e) * D : (int64_t)(p.NH + h) * D;
+      xe[s] = *reinterpret_cast<const uint4*>(row + col);
+      we[s] = *reinterpret_cast<const uint4*>((e < G ? p.qn_w : p.kn_w) + 8 * c);
+    }
     xv = *reinterpret_cast<const uint4*>(row + (int64_t)(p.NH + p.NKV + h) * D);
-    wq = *reinterpret_cast<const uint4*>(p.qn_w + 8 * c);
-    wk = *reinterpret_cast<const uint4*>(p.kn_w + 8 * c);
     rc = *reinterpret_cast<const uint4*>(p.cos + (int64_t)b * p.cs_sb + 8 * c);
     rs = *reinterpret_cast<const uint4*>(p.sin + (int64_t)b * p.cs_sb + 8 * c);
     newpos64 = p.cache_pos[0];
@@ -533,9 +560,16 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   uint4 qp[G], knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
   int newpos = -1;
   if (FUSED) {
+    uint4 ye[NS];
 #pragma unroll
-    for (int g = 0; g < G; ++g) qp[g] = norm_rope8<LPR>(xq[g], wq, rc, rs, p.eps, c);
-    knew = norm_rope8<LPR>(xk, wk, rc, rs, p.eps, c);
+    for (int s = 0; s < NS; ++s) ye[s] = norm_rope8<LPR>(xe[s], we[s], rc, rs, p.eps, c);
+    static_assert(RPW * LPR == kWave, "a wave holds whole rows");
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const uint4 y = lane_fetch4(ye[e / RPW], (e % RPW) * LPR + c);  // head e from lane c of row e % RPW
+      if (e < G) qp[e] = y;
+      else knew = y;
+    }
     vnew = xv;
     if (newpos64 >= 0 && newpos64 < p.cap) {
       const int pos = (int)newpos64;
@@ -725,7 +759,8 @@ SplitFn pick_group(int G, int mk, int ppt) {
     case 1: return pick_mask<D, 1, NT, FUSED>(mk, ppt);
     case 2: return pick_mask<D, 2, NT, FUSED>(mk, ppt);
     case 4: return pick_mask<D, 4, NT, FUSED>(mk, ppt);
-    case 8: return pick_mask<D, 8, NT, FUSED>(mk, ppt);
+    // G = 8 runs with 256 threads only (the host never picks 512 for it: its accumulators would not fit in VGPRs)
+    case 8: if constexpr (NT == 256) return pick_mask<D, 8, NT, FUSED>(mk, ppt); else return nullptr;
     default: return nullptr;
   }
 }
