@@ -38,6 +38,8 @@ def parse_args():
     p.add_argument("--eager", action="store_true", help="launch each call from Python instead of a HIP graph")
     p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4],
                    help="headline workload (BASELINE config; 2 is the metric's serving shape)")
+    p.add_argument("--fused", action="store_true",
+                   help="time the fused decode step (bz_gqa_decode_fused) instead of attention alone")
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--traffic-bytes", type=float, default=None,
@@ -53,13 +55,38 @@ def _pkg():
     return __graft_entry__.package()
 
 
-def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold):
-    """µs per call for workload w (one q per call) over `steps` calls; cold rotates distinct K/V buffer sets."""
+def fused_inputs(w, dev):
+    """Raw q | k | v projections, norm weights and RoPE tables for a fused step at slot seq_len - 1 of workload w
+    (seeded; the new token of a decode step whose cache already holds seq_len - 1 positions)."""
+    import torch
+
+    B, NH, NKV, D = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim
+    L = int(w.seq_lens[0])
+    if any(int(x) != L for x in w.seq_lens):
+        raise ValueError("a fused step needs one length for every row")
+    gen = torch.Generator().manual_seed(100 + L)
+    qkv = (torch.randn(B, (NH + 2 * NKV) * D, generator=gen) * 3).to(torch.bfloat16).to(dev)
+    qn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(dev)
+    kn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(dev)
+    inv = 1e6 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = torch.cat([(L - 1) * inv] * 2)
+    cos = ang.cos().to(torch.bfloat16).expand(B, D).contiguous().to(dev)
+    sin = ang.sin().to(torch.bfloat16).expand(B, D).contiguous().to(dev)
+    cache_pos = torch.tensor([L - 1], dtype=torch.int64, device=dev)
+    return qkv, qn, kn, cos, sin, cache_pos
+
+
+def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=False):
+    """µs per call for workload w (one q per call) over `steps` calls; cold rotates distinct K/V buffer sets.
+    fused: each call is a fused decode step (bz_gqa_decode_fused) writing slot seq_len - 1 of its set (the same
+    values every time) and attending over it."""
     import torch
     from breeze_tts_2_flash_amd import workloads
 
     g = w.to(dev)
-    read_bytes = workloads.algorithmic_bytes(w.seq_lens.tolist(), w.num_q_heads, w.num_kv_heads, w.head_dim)
+    lens = w.seq_lens.tolist()
+    nb = workloads.fused_algorithmic_bytes if fused else workloads.algorithmic_bytes
+    read_bytes = nb(lens, w.num_q_heads, w.num_kv_heads, w.head_dim)
     nsets = max(16, math.ceil(640e6 / read_bytes)) if cold else 1
     nsets = min(nsets, steps)
     ks = torch.empty((nsets,) + tuple(g.k.shape), dtype=g.k.dtype, device=dev)
@@ -67,10 +94,19 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold):
     ks.copy_(g.k.expand_as(ks))
     vs.copy_(g.v.expand_as(vs))
     out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
-    kw = dict(out=out, combine=combine, num_splits=splits)
+    kw = dict(combine=combine, num_splits=splits)
+    if fused:
+        qkv, qn, kn, cos, sin, cache_pos = fused_inputs(w, dev)
+
+        def run(k, v, o=None):
+            return pkg.gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, k, v, cache_pos, g.scale, o, seq_lens=g.seq_lens,
+                                        **kw)
+    else:
+        def run(k, v, o=None):
+            return pkg.gqa_decode(g.q, k, v, g.seq_lens, g.scale, o, **kw)
 
     def call(i):
-        pkg.gqa_decode(g.q, ks[i % nsets], vs[i % nsets], g.seq_lens, g.scale, **kw)
+        run(ks[i % nsets], vs[i % nsets], out)
 
     for i in range(warmup):
         call(i)
@@ -96,65 +132,12 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold):
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1000.0 / steps
     # the rotated sets hold identical data: the last call's output must equal a fresh call on set 0
-    ref = pkg.gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, combine=combine, num_splits=splits)
+    ref = run(ks[0], vs[0])
     torch.cuda.synchronize()
     if not torch.equal(out.view(torch.int16), ref.view(torch.int16)):
         raise RuntimeError("benchmark output differs from a direct call")
     del ks, vs
     return us, read_bytes, nsets
-
-
-def time_fused(pkg, w, dev, steps, warmup, splits):
-    """µs per fused decode step (bz_gqa_decode_fused) on workload w: the token at slot seq_len - 1 is normed, roped,
-    written into the cache and attended, as the reference's decode step calls attn_decode_fused. Cold rotation over
-    K/V sets as in time_calls (every call rewrites the same slot of its set with the same values)."""
-    import torch
-    from breeze_tts_2_flash_amd import workloads
-
-    g = w.to(dev)
-    B, NH, NKV, D = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim
-    L = int(w.seq_lens[0])
-    if any(int(x) != L for x in w.seq_lens):
-        raise ValueError("time_fused needs one length for every row")
-    gen = torch.Generator().manual_seed(100 + L)
-    qkv = (torch.randn(B, (NH + 2 * NKV) * D, generator=gen) * 3).to(torch.bfloat16).to(dev)
-    qn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(dev)
-    kn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(dev)
-    inv = 1e6 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
-    ang = torch.cat([(L - 1) * inv] * 2)
-    cos = ang.cos().to(torch.bfloat16).expand(B, D).contiguous().to(dev)
-    sin = ang.sin().to(torch.bfloat16).expand(B, D).contiguous().to(dev)
-    cache_pos = torch.tensor([L - 1], dtype=torch.int64, device=dev)
-    nbytes = workloads.fused_algorithmic_bytes(w.seq_lens.tolist(), NH, NKV, D)
-    nsets = min(steps, max(16, math.ceil(640e6 / nbytes)))
-    ks = torch.empty((nsets,) + tuple(g.k.shape), dtype=g.k.dtype, device=dev)
-    vs = torch.empty_like(ks)
-    ks.copy_(g.k.expand_as(ks))
-    vs.copy_(g.v.expand_as(vs))
-    out = torch.empty(B, NH, D, dtype=torch.bfloat16, device=dev)
-
-    def call(i):
-        pkg.gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, ks[i % nsets], vs[i % nsets], cache_pos, g.scale, out,
-                             seq_lens=g.seq_lens, num_splits=splits)
-
-    for i in range(warmup):
-        call(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            call(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    graph.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1000.0 / steps
-    del ks, vs
-    return us, nbytes, nsets
 
 
 def time_depth_frame(pkg, dev, steps, warmup):
@@ -282,14 +265,15 @@ def main():
     print(f"[bench] config {cfg} cold, {args.steps} calls, splits={splits2}, combine={args.combine}", file=sys.stderr,
           flush=True)
     us, nbytes, nsets = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
-                                   cold=True)
+                                   cold=True, fused=args.fused)
     gbs = nbytes / us / 1e3
     print(f"[bench] config {cfg} cold: {us:.3f} us/call, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": WORKLOADS[cfg],
+        "config": {"workload": WORKLOADS[cfg] + (" (fused step: q/k RMSNorm + RoPE + cache write + attention)"
+                                                 if args.fused else ""),
                    "us_per_call": round(us, 3), "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                    "storage": "bf16", "splits": splits2, "combine": args.combine,
                    "timing": "eager launches" if args.eager else "HIP graph replay, HIP events on the launch stream",
@@ -297,12 +281,12 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": args.traffic_bytes if args.traffic_bytes is not None else
-                     (traffic_from_profile() if cfg == 2 else None)},
+                     (traffic_from_profile() if cfg == 2 and not args.fused else None)},
     }
     extra = {}
     if not args.no_extra:
         us_w, _, _ = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
-                                cold=False)
+                                cold=False, fused=args.fused)
         extra[f"config{cfg}_warm"] = {"us_per_call": round(us_w, 3), "GB/s": round(nbytes / us_w / 1e3, 1)}
         print(f"[bench] config {cfg} warm: {us_w:.3f} us/call", file=sys.stderr, flush=True)
         for xc in (2, 3, 4):
@@ -317,8 +301,9 @@ def main():
             print(f"[bench] config {xc} cold: {us_c:.3f} us/call, {nb / us_c / 1e3:.1f} GB/s", file=sys.stderr,
                   flush=True)
             del w
-        if w2.head_dim == 128 and len(set(w2.seq_lens.tolist())) == 1:
-            us_x, nbx, nsx = time_fused(pkg, w2, dev, args.steps, args.warmup, args.splits)
+        if not args.fused and w2.head_dim == 128 and len(set(w2.seq_lens.tolist())) == 1:
+            us_x, nbx, nsx = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
+                                        cold=True, fused=True)
             extra[f"config{cfg}_fused_cold"] = {
                 "entry": "bz_gqa_decode_fused (q/k RMSNorm + RoPE + cache-slot write + attention)",
                 "us_per_call": round(us_x, 3), "GB/s": round(nbx / us_x / 1e3, 1),

@@ -12,6 +12,7 @@ from .attention import (default_splits, get_workspace, gqa_decode, gqa_decode_fu
                         workspace_bytes)
 from .compat import attn_decode, attn_decode_fused
 from .kernels import build, load
+from . import hf_attention
 
 __all__ = ["gqa_decode", "gqa_decode_masked", "gqa_decode_fused", "attn_decode", "attn_decode_fused",
            "workspace_bytes", "default_splits", "get_workspace", "build", "load"]
