@@ -70,26 +70,27 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
-def _q_view(q: torch.Tensor) -> tuple[int, int, int, int, int]:
-    """(B, NH, D, stride_b, stride_h) of a query given as [B, NH, D] or [B, NH, 1, D]."""
+def _q_view(q: torch.Tensor) -> tuple[int, int, int, int, int, int, int]:
+    """(B, NH, T, D, stride_b, stride_h, stride_t) of a query given as [B, NH, D] or [B, NH, T, D] (the transformers
+    layout, query tokens in dim 2; T = 1 for a plain decode step)."""
     if q.dim() == 4:
-        _check(q.size(2) == 1, f"query must have q_len == 1, got shape {tuple(q.shape)}")
-        return q.size(0), q.size(1), q.size(3), q.stride(0), q.stride(1)
-    _check(q.dim() == 3, f"query must be [B, NH, D] or [B, NH, 1, D], got shape {tuple(q.shape)}")
-    return q.size(0), q.size(1), q.size(2), q.stride(0), q.stride(1)
+        return q.size(0), q.size(1), q.size(2), q.size(3), q.stride(0), q.stride(1), q.stride(2)
+    _check(q.dim() == 3, f"query must be [B, NH, D] or [B, NH, T, D], got shape {tuple(q.shape)}")
+    return q.size(0), q.size(1), 1, q.size(2), q.stride(0), q.stride(1), 0
 
 
-def _out_view(out: torch.Tensor, B: int, NH: int, D: int) -> tuple[int, int]:
-    """(stride_b, stride_h) of an output given as [B, NH, D], [B, 1, NH, D] (reference layout) or [B, NH, 1, D]."""
+def _out_view(out: torch.Tensor, B: int, NH: int, T: int, D: int) -> tuple[int, int, int]:
+    """(stride_b, stride_h, stride_t) of an output given as [B, T, NH, D] (the reference's layout, T = 1 for
+    attn_decode) or [B, NH, T, D]; with T = 1 also [B, NH, D]."""
     _check(out.dtype == torch.bfloat16, "out must be bf16")
     _check(out.stride(-1) == 1, "out's last dimension must be contiguous")
-    if out.dim() == 4 and tuple(out.shape) == (B, 1, NH, D):
-        return out.stride(0), out.stride(2)
-    if out.dim() == 4 and tuple(out.shape) == (B, NH, 1, D):
-        return out.stride(0), out.stride(1)
-    _check(out.dim() == 3 and tuple(out.shape) == (B, NH, D),
-           f"out must be [B, NH, D], [B, 1, NH, D] or [B, NH, 1, D] with B={B}, NH={NH}, D={D}")
-    return out.stride(0), out.stride(1)
+    if out.dim() == 4 and tuple(out.shape) == (B, T, NH, D):
+        return out.stride(0), out.stride(2), out.stride(1)
+    if out.dim() == 4 and tuple(out.shape) == (B, NH, T, D):
+        return out.stride(0), out.stride(1), out.stride(2)
+    _check(T == 1 and out.dim() == 3 and tuple(out.shape) == (B, NH, D),
+           f"out must be [B, T, NH, D], [B, NH, T, D] or (T = 1) [B, NH, D] with B={B}, T={T}, NH={NH}, D={D}")
+    return out.stride(0), out.stride(1), 0
 
 
 def _mask_view(mask: torch.Tensor, B: int, cap: int) -> tuple[int, int]:
@@ -108,18 +109,20 @@ def _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine
            "query, k_cache and v_cache must be bf16")
     _check(k_cache.device == q.device and v_cache.device == q.device, "all tensors must be on one device")
     _check(q.stride(-1) == 1, "query's head_dim must be contiguous")
-    B, NH, D, q_sb, q_sh = _q_view(q)
+    B, NH, T, D, q_sb, q_sh, q_st = _q_view(q)
     _check(k_cache.dim() == 4 and v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
            "k_cache and v_cache must be [B, NKV, capacity, D] with equal shapes and strides")
     _check(k_cache.size(0) == B and k_cache.size(3) == D and k_cache.stride(3) == 1,
            f"k_cache {tuple(k_cache.shape)} does not match query {tuple(q.shape)}")
     NKV, cap = k_cache.size(1), k_cache.size(2)
     if out is None:
-        out = torch.empty(B, NH, D, dtype=torch.bfloat16, device=q.device)
+        shape = (B, NH, D) if T == 1 else (B, T, NH, D)
+        out = torch.empty(shape, dtype=torch.bfloat16, device=q.device)
     _check(out.device == q.device, "out must be on the query's device")
-    o_sb, o_sh = _out_view(out, B, NH, D)
+    o_sb, o_sh, o_st = _out_view(out, B, NH, T, D)
     a = kernels.GqaDecodeArgs()
     a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q_sb, q_sh
+    a.tokens_per_row, a.q_stride_t, a.out_stride_t = T, q_st, o_st
     a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
     a.kv_stride_b, a.kv_stride_h, a.kv_stride_s = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
     a.scale = float(scale)
@@ -141,10 +144,12 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
                combine: str | int = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:
     """GQA decode attention over [kv_start[b], seq_lens[b]) of a bf16 KV cache.
 
-    q: [B, NH, D] or [B, NH, 1, D] bf16 (head_dim contiguous); k_cache, v_cache: [B, NKV, capacity, D] bf16;
+    q: [B, NH, D] or [B, NH, T, D] bf16 (head_dim contiguous); k_cache, v_cache: [B, NKV, capacity, D] bf16;
     seq_lens: [B] int32 (exclusive end); kv_start: [B] int32 or None; mask: optional additive mask
     [B or 1, 1, 1, >= capacity] (bf16 or fp32) applied inside the range (<= -1e30 excludes a position);
-    out: [B, NH, D] (default), [B, 1, NH, D] or [B, NH, 1, D] bf16. Returns out.
+    out: [B, NH, D] (default for T = 1), [B, T, NH, D] (default for T > 1) or [B, NH, T, D] bf16. Returns out.
+    With T > 1 query tokens, row b's tokens are its last T positions, causal among themselves: token t attends
+    [kv_start[b], seq_lens[b] - (T - 1 - t)) (the depth transformer's first step, depth_frame.cu:221-227).
     """
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
@@ -156,7 +161,8 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
         a.mask = mask.data_ptr()
     with torch.cuda.device(dev):
         ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity, a.num_splits, a.max_seq_len)
+            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
+            a.num_splits, a.max_seq_len)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
         stream = torch.cuda.current_stream(dev).cuda_stream
         kernels.check(kernels.load().bz_gqa_decode(ctypes.byref(a), ctypes.c_void_p(stream)), "bz_gqa_decode")
@@ -175,7 +181,8 @@ def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     a.mask = mask.data_ptr()
     with torch.cuda.device(dev):
         ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity, a.num_splits, a.max_seq_len)
+            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
+            a.num_splits, a.max_seq_len)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
         stream = torch.cuda.current_stream(dev).cuda_stream
         kernels.check(kernels.load().bz_gqa_decode_masked(ctypes.byref(a), ctypes.c_void_p(stream)),
@@ -231,7 +238,8 @@ def gqa_decode_fused(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
     f.cache_pos = cache_pos.data_ptr()
     with torch.cuda.device(dev):
         ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity, a.num_splits, a.max_seq_len)
+            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
+            a.num_splits, a.max_seq_len)
         f.base.workspace, f.base.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
         stream = torch.cuda.current_stream(dev).cuda_stream
         kernels.check(kernels.load().bz_gqa_decode_fused(ctypes.byref(f), ctypes.c_void_p(stream)),

@@ -118,6 +118,10 @@ int check_sizes(int B, int NH, int NKV, int D, int cap) {
   return BZ_OK;
 }
 
+// Query tokens per row (0 in the struct means 1) and the number of (row, token) pairs, the kernels' grid rows.
+int tokens_of(const bz_gqa_decode_args* a) { return a->tokens_per_row > 1 ? a->tokens_per_row : 1; }
+int rows_of(const bz_gqa_decode_args* a) { return a->batch * tokens_of(a); }
+
 int resolve_splits(const bz_gqa_decode_args* a, int* splits) {
   if (a->num_splits < 0 || a->num_splits > kMaxSplits) return BZ_ERR_SHAPE;
   if (a->num_splits > 0) {
@@ -127,7 +131,7 @@ int resolve_splits(const bz_gqa_decode_args* a, int* splits) {
   int cus = 0;
   const int rc = device_cus(&cus);
   if (rc != BZ_OK) return rc;
-  *splits = default_splits_for(a->batch * a->num_kv_heads, a->head_dim,
+  *splits = default_splits_for(rows_of(a) * a->num_kv_heads, a->head_dim,
                                effective_len(a->capacity, a->max_seq_len), cus);
   return BZ_OK;
 }
@@ -137,12 +141,12 @@ int resolve_splits(const bz_gqa_decode_args* a, int* splits) {
 int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
            int mask_kind, const bz_gqa_decode_fused_args* f) {
   const int B = a->batch, NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
-  const int G = NH / NKV;
+  const int G = NH / NKV, T = tokens_of(a), R = rows_of(a);
   int splits = 0;
   int rc = resolve_splits(a, &splits);
   if (rc != BZ_OK) return rc;
   if (a->combine < BZ_COMBINE_AUTO || a->combine > BZ_COMBINE_KERNEL) return BZ_ERR_COMBINE_MODE;
-  const WsLayout ws = ws_layout(B, NH, NKV, D, splits);
+  const WsLayout ws = ws_layout(R, NH, NKV, D, splits);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
 
@@ -153,7 +157,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   int cus = 0;
   rc = device_cus(&cus);
   if (rc != BZ_OK) return rc;
-  const int nt = threads_for(D, G, chunk, (int64_t)splits * NKV * B, cus);
+  const int nt = threads_for(D, G, chunk, (int64_t)splits * NKV * R, cus);
   const int ppt = ppt_for(D, G, chunk, nt);
   SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt, f != nullptr);
   SplitFn comb_fn = pick_combine(D, G);
@@ -164,6 +168,8 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
   p.q_sh = a->q_stride_h;
+  p.q_st = a->q_stride_t;
+  p.T = T;
   p.k = static_cast<const uint16_t*>(a->k_cache);
   p.v = static_cast<const uint16_t*>(a->v_cache);
   p.kv_sb = a->kv_stride_b;
@@ -177,6 +183,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   p.out = static_cast<uint16_t*>(a->out);
   p.o_sb = a->out_stride_b;
   p.o_sh = a->out_stride_h;
+  p.o_st = a->out_stride_t;
   p.B = B;
   p.NH = NH;
   p.NKV = NKV;
@@ -209,10 +216,10 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
     p.v_out = const_cast<uint16_t*>(p.v);
   }
 
-  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, B), dim3(nt), 0, stream, p);
+  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, R), dim3(nt), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
   if (two_kernels && splits > 1) {
-    hipLaunchKernelGGL(comb_fn, dim3(NKV, B), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(comb_fn, dim3(NKV, R), dim3(kThreads), 0, stream, p);
     if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
   }
   return BZ_OK;
@@ -228,6 +235,7 @@ int check_common(const bz_gqa_decode_args* a, bool need_q) {
   if ((kp | vp) & 15) return BZ_ERR_ALIGNMENT;
   if ((a->kv_stride_b | a->kv_stride_h | a->kv_stride_s) & 7) return BZ_ERR_ALIGNMENT;
   if (a->kv_stride_s < a->head_dim) return BZ_ERR_SHAPE;
+  if (a->tokens_per_row < 0 || (int64_t)a->batch * tokens_of(a) > 65535) return BZ_ERR_SHAPE;  // grid.z limit
   // K/V are read through buffer resources with 32-bit byte offsets per (row, kv head): every offset the kernel forms
   // (positions below capacity + 1024, the largest read-ahead) must stay below 2^31
   if (((int64_t)a->capacity + 1024) * a->kv_stride_s * 2 > INT32_MAX) return BZ_ERR_SHAPE;
@@ -242,7 +250,7 @@ int mask_ranges(const bz_gqa_decode_args* a, hipStream_t stream, int32_t** start
   int splits = 0;
   int rc = resolve_splits(a, &splits);
   if (rc != BZ_OK) return rc;
-  const WsLayout ws = ws_layout(a->batch, a->num_q_heads, a->num_kv_heads, a->head_dim, splits);
+  const WsLayout ws = ws_layout(rows_of(a), a->num_q_heads, a->num_kv_heads, a->head_dim, splits);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
   int32_t* ranges = reinterpret_cast<int32_t*>(static_cast<char*>(a->workspace) + ws.ranges);
@@ -266,7 +274,7 @@ int check_fused(const bz_gqa_decode_fused_args* f) {
   if (f->qkv == nullptr || f->q_norm_weight == nullptr || f->k_norm_weight == nullptr || f->cos == nullptr ||
       f->sin == nullptr || f->cache_pos == nullptr)
     return BZ_ERR_NULL;
-  if (a->head_dim != 128) return BZ_ERR_UNSUPPORTED;
+  if (a->head_dim != 128 || tokens_of(a) != 1) return BZ_ERR_UNSUPPORTED;
   if (f->qkv_stride_b < (int64_t)(a->num_q_heads + 2 * a->num_kv_heads) * a->head_dim) return BZ_ERR_SHAPE;
   if (f->rope_stride_b < a->head_dim) return BZ_ERR_SHAPE;
   const uintptr_t ptrs = reinterpret_cast<uintptr_t>(f->qkv) | reinterpret_cast<uintptr_t>(f->q_norm_weight) |

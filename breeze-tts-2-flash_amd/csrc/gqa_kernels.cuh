@@ -36,7 +36,8 @@ namespace bz {
 
 struct Params {
   const uint16_t* q;
-  int64_t q_sb, q_sh;
+  int64_t q_sb, q_sh, q_st;  // batch, head and token strides of q
+  int T;                     // query tokens per row (the last T positions of the row, causal among themselves)
   const uint16_t* k;
   const uint16_t* v;
   int64_t kv_sb, kv_sh, kv_ss;
@@ -46,12 +47,12 @@ struct Params {
   int64_t m_sb;
   float scale_log2;  // scale * log2(e)
   uint16_t* out;
-  int64_t o_sb, o_sh;
+  int64_t o_sb, o_sh, o_st;
   int B, NH, NKV, cap, splits, min_chunk;
   int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
-  float* part_acc;   // [B, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
-  float2* part_ml;   // [B, NH, splits]     (m, sum_p 2^(s_p - m))
-  int* counters;     // [B, NKV] x kCounterStride arrivals, reset by the merging workgroup
+  float* part_acc;   // [B * T, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
+  float2* part_ml;   // [B * T, NH, splits]     (m, sum_p 2^(s_p - m))
+  int* counters;     // [B * T, NKV] x kCounterStride arrivals, reset by the merging workgroup
   // fused prologue only
   const uint16_t* qkv;  // [B, (NH + 2 NKV) * D] raw projections: q heads | k heads | v heads
   int64_t qkv_sb;
@@ -232,6 +233,13 @@ __device__ __forceinline__ void row_range(const Params& p, int b, int& start, in
   end = e;
 }
 
+// Range of query token t of row b: the row's tokens are its last T positions, each attending up to itself, so token
+// t ends T - 1 - t positions before the row (flash/csrc/depth_frame.cu:221-227: token t of step 0 attends 0..t).
+__device__ __forceinline__ void token_range(const Params& p, int b, int t, int& start, int& end) {
+  row_range(p, b, start, end);
+  end = max(start, end - (p.T - 1 - t));
+}
+
 // Positions per split and number of non-empty splits for a row of length len (>= 1 split even when empty, so
 // that someone writes the row's output).
 __device__ __forceinline__ int split_chunk(int len, int splits, int min_chunk) {
@@ -278,14 +286,16 @@ __device__ __forceinline__ float ld_agent(const float* ptr) {
 // w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s are reduced over the wave with DPP and lane swaps and stored to LDS
 // zero-padded, so the weighted sum over the first kBatch splits needs no per-split condition.
 template <int D, int G, int NT>
-__device__ void merge_splits(const Params& p, int b, int h, int nact) {
+__device__ void merge_splits(const Params& p, int z, int h, int nact) {
   constexpr int kBatch = 32;
   constexpr int NW = NT / kWave;
   constexpr int kOut = (G * D + NT - 1) / NT;
   constexpr int kPerLane = kMaxSplits / kWave;
   __shared__ __align__(16) float s_w[G][kMaxSplits];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int64_t row0 = (int64_t)b * p.NH + h * G;  // first q head of the group, as a [B * NH] row index
+  const int64_t row0 = (int64_t)z * p.NH + h * G;  // first q head of the group, as a [B * T * NH] row index
+  const int b = z / p.T, tok = z - b * p.T;
+  uint16_t* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)tok * p.o_st;
 
   float t[kOut][kBatch];
 #pragma unroll
@@ -345,7 +355,7 @@ __device__ void merge_splits(const Params& p, int b, int h, int nact) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][s0 + u], x[u], a);
     }
-    p.out[(int64_t)b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
+    orow[(int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
   }
 }
 
@@ -488,7 +498,8 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   constexpr int RPW = kWave / LPR;      // rows per wave
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
 
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, h = blockIdx.y, z = blockIdx.z;  // z = row * T + token
+  const int b = z / p.T, tok = z - b * p.T;
   const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
 
   // q of the G heads of this group, this lane's 8 dims, issued first, since none of it depends on the row's length.
@@ -518,14 +529,14 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   } else {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const uint16_t* qsrc = p.q + (int64_t)b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + 8 * c;
+      const uint16_t* qsrc = p.q + (int64_t)b * p.q_sb + (int64_t)tok * p.q_st + (int64_t)(h * G + g) * p.q_sh + 8 * c;
 #pragma unroll
       for (int j = 0; j < 8; ++j) qh[g][j] = qsrc[j];
     }
   }
 
   int start, end;
-  row_range(p, b, start, end);
+  token_range(p, b, tok, start, end);
   const int len = end - start;
   const int chunk = split_chunk(len, p.splits, p.min_chunk);
   const int nact = split_count(len, chunk);
@@ -657,9 +668,10 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
       A = fmaf(e, s_acc[u][g][d], A);
     }
     if (nact == 1) {
-      p.out[(int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d] = f32_to_bf16(L > 0.f ? A / L : 0.f);
+      p.out[(int64_t)b * p.o_sb + (int64_t)tok * p.o_st + (int64_t)hq * p.o_sh + d] =
+          f32_to_bf16(L > 0.f ? A / L : 0.f);
     } else {
-      const int64_t ps = ((int64_t)b * p.NH + hq) * p.splits + split;
+      const int64_t ps = ((int64_t)z * p.NH + hq) * p.splits + split;
       st_agent(p.part_acc + ps * D + d, A);
       if (d == 0) {
         st_agent(reinterpret_cast<float*>(p.part_ml + ps), M);
@@ -677,26 +689,26 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
   if (tid == 0) {
-    int* cnt = p.counters + (b * p.NKV + h) * kCounterStride;
+    int* cnt = p.counters + ((int64_t)z * p.NKV + h) * kCounterStride;
     const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == nact - 1);
     if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
-  merge_splits<D, G, NT>(p, b, h, nact);
+  merge_splits<D, G, NT>(p, z, h, nact);
 }
 
 // Second-launch merge: one workgroup per (kv head, row).
 template <int D, int G>
 __global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
-  const int h = blockIdx.x, b = blockIdx.y;
+  const int h = blockIdx.x, z = blockIdx.y;  // z = row * T + token
   int start, end;
-  row_range(p, b, start, end);
+  token_range(p, z / p.T, z % p.T, start, end);
   const int len = end - start;
   const int nact = split_count(len, split_chunk(len, p.splits, p.min_chunk));
   if (nact == 1) return;  // the split kernel wrote the output
-  merge_splits<D, G, kThreads>(p, b, h, nact);
+  merge_splits<D, G, kThreads>(p, z, h, nact);
 }
 
 // Interval of the additive mask row: first and last position with value > -1e30.

@@ -30,7 +30,7 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
@@ -56,6 +56,7 @@ class GqaDecodeArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int32), ("capacity", ctypes.c_int32),
         ("num_splits", ctypes.c_int32), ("max_seq_len", ctypes.c_int32), ("combine", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("tokens_per_row", ctypes.c_int32), ("q_stride_t", ctypes.c_int64), ("out_stride_t", ctypes.c_int64),
     ]
 
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 2
+#define BZ_GQA_DECODE_ABI_VERSION 3
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -93,6 +93,13 @@ typedef struct bz_gqa_decode_args {
      zero-filled once before first use; the library leaves it ready for the next call. */
   void* workspace;
   size_t workspace_bytes;
+  /* Query tokens per row, T (0 or 1: one). With T > 1 each row carries its last T positions as queries, causal
+     among themselves (the depth transformer's first step, flash/csrc/depth_frame.cu:221-227): token t of row b
+     attends [kv_start[b], seq_lens[b] - (T - 1 - t)). q element (b, t, h, d) is at q[b*q_stride_b + t*q_stride_t +
+     h*q_stride_h + d], out element (b, t, h, d) at out[b*out_stride_b + t*out_stride_t + h*out_stride_h + d]. The
+     workspace and the default split count are those of batch * T rows. bz_gqa_decode_fused takes T = 1 only. */
+  int32_t tokens_per_row;
+  int64_t q_stride_t, out_stride_t;
 } bz_gqa_decode_args;
 
 /* GQA decode attention. Replaces the reference op attn_decode (flash/csrc/bb_attn.cu:416-429, pybind :463-465)
@@ -100,12 +107,14 @@ typedef struct bz_gqa_decode_args {
    start the reference encodes in its interval mask (backbone_graph.py:239-252). */
 int bz_gqa_decode(const bz_gqa_decode_args* args, hipStream_t stream);
 
-/* Bytes of workspace bz_gqa_decode needs for these sizes (num_splits as passed, 0 = default). Replaces the
-   caller-side sizing of the reference's scores/cmax/part/counters buffers (flash/backbone.py:27-37). */
+/* Bytes of workspace bz_gqa_decode needs for these sizes (num_splits as passed, 0 = default; with tokens_per_row
+   T > 1 pass batch * T). Replaces the caller-side sizing of the reference's scores/cmax/part/counters buffers
+   (flash/backbone.py:27-37). */
 int bz_gqa_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                                  int32_t capacity, int32_t num_splits, int32_t max_seq_len, size_t* bytes);
 
-/* The split count bz_gqa_decode uses when num_splits == 0 (device CU count, sizes). No counterpart in the
+/* The split count bz_gqa_decode uses when num_splits == 0 (device CU count, sizes; with tokens_per_row T > 1 pass
+   batch * T). No counterpart in the
    reference, which fixes 64-position chunks at compile time (bb_attn.cu:28, :382). */
 int bz_gqa_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t capacity,
                                  int32_t max_seq_len, int32_t* num_splits);

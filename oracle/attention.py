@@ -87,6 +87,24 @@ def sdpa_fp32(q, k, v, seq_lens, scale: float, kv_start=None):
     return out
 
 
+def decode_attention_tokens(q, k, v, seq_lens, scale: float, kv_start=None, mask=None) -> np.ndarray:
+    """T query tokens per row, causal among themselves: the row's tokens are its last T positions and token t
+    attends [start, end - (T - 1 - t)) (the depth transformer's first step, flash/csrc/depth_frame.cu:221-227:
+    token t of step 0 attends positions 0..t). q [B, NH, T, D]; k, v, seq_lens, kv_start, mask as decode_attention.
+    Returns float64 [B, T, NH, D]."""
+    q = np.asarray(q, dtype=np.float64)
+    B, NH, T, D = q.shape
+    cap = np.asarray(k).shape[2]
+    out = np.zeros((B, T, NH, D), dtype=np.float64)
+    for t in range(T):
+        ends = np.zeros(B, dtype=np.int64)
+        for b in range(B):
+            start, end = _row_range(b, seq_lens, kv_start, cap)
+            ends[b] = max(start, end - (T - 1 - t))
+        out[:, t] = decode_attention(q[:, :, t], k, v, ends, scale, kv_start=kv_start, mask=mask)
+    return out
+
+
 def repeat_kv(x, n_rep: int):
     """torch [B, NKV, S, D] -> [B, NKV * n_rep, S, D] (models/breeze.py:245-256)."""
     if n_rep == 1:

@@ -121,6 +121,9 @@ def _good_args(K, **over):
     # 31-bit byte offsets inside one (row, kv head) span: (capacity + 1024) * kv_stride_s * 2 < 2^31
     (dict(capacity=(1 << 23) - 1024, num_splits=4), -2), (dict(capacity=1 << 20, kv_stride_s=1024), -2),
     (dict(capacity=(1 << 23) - 1025, num_splits=4), -5),   # just inside the bound: fails later, on the workspace
+    # query tokens per row: >= 0, and batch * tokens within the grid's z limit
+    (dict(tokens_per_row=-1), -2), (dict(batch=16384, tokens_per_row=4), -2),
+    (dict(batch=16383, tokens_per_row=4), -5), (dict(tokens_per_row=0), -5), (dict(tokens_per_row=3), -5),
 ])
 def test_host_validation(lib, K, over, code):
     a = _good_args(K, **over)
@@ -180,6 +183,7 @@ def _good_fused(K, **over):
     (dict(qkv_stride_b=100), -2), (dict(rope_stride_b=64), -2),
     (dict(qkv=0x70008), -4), (dict(cos=0x73004), -4), (dict(qkv_stride_b=32 * 128 + 4), -4),
     (dict(cache_pos=0x75004), -4),
+    (dict(base_tokens_per_row=2), -3),                        # the fused step has one query token per row
     (dict(), -5),                                             # no workspace (checked before any launch)
     (dict(base_seq_lens=None), -1),                           # interval form needs a mask
 ])
