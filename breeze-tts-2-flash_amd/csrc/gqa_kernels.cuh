@@ -254,6 +254,73 @@ __device__ __forceinline__ float load_mask(const void* m, int64_t off) {
   return static_cast<const float*>(m)[off];
 }
 
+// v_permlane16_swap / v_permlane32_swap on two registers: rows 1 and 3 (16 lanes each) of a trade places with rows
+// 0 and 2 of b (swap16); lanes 32..63 of a trade places with lanes 0..31 of b (swap32). With rows written
+// [r0 r1 r2 r3]: swap16 turns a, b into [a0 b0 a2 b2], [a1 b1 a3 b3]; swap32 into [a0 a1 b0 b1], [a2 a3 b2 b3].
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+// Transposed sum over the four 16-lane rows of a wave: returns x with row r of x holding v_r summed over all four rows
+// (three swaps and three adds for four values, against two swaps and two adds per value for a broadcast sum).
+__device__ __forceinline__ float rows_sum4(float v0, float v1, float v2, float v3) {
+  swap16(v0, v1);
+  swap16(v2, v3);
+  float s = v0 + v1;  // [v0(01) v1(01) v0(23) v1(23)]
+  float t = v2 + v3;  // [v2(01) v3(01) v2(23) v3(23)]
+  swap32(s, t);
+  return s + t;       // [v0 v1 v2 v3], each summed over the four rows
+}
+
+// Max over the four 16-lane rows of a wave of each of the N values x[i]; every lane ends with all N maxima.
+template <int N>
+__device__ __forceinline__ void rows_max(float (&x)[N]) {
+  if constexpr (N == 1) {
+    float y = x[0];
+    swap16(x[0], y);
+    x[0] = fmaxf(x[0], y);
+    y = x[0];
+    swap32(x[0], y);
+    x[0] = fmaxf(x[0], y);
+  } else if constexpr (N == 2) {
+    swap16(x[0], x[1]);
+    float s = fmaxf(x[0], x[1]);  // [A(01) B(01) A(23) B(23)]
+    float t = s;
+    swap32(s, t);
+    s = fmaxf(s, t);              // [A B A B]
+    t = s;
+    swap16(s, t);                 // [A A A A], [B B B B]
+    x[0] = s;
+    x[1] = t;
+  } else {
+    static_assert(N % 4 == 0, "rows_max: 1, 2 or a multiple of 4 values");
+#pragma unroll
+    for (int q = 0; q < N; q += 4) {
+      swap16(x[q], x[q + 1]);
+      swap16(x[q + 2], x[q + 3]);
+      float s = fmaxf(x[q], x[q + 1]), t = fmaxf(x[q + 2], x[q + 3]);
+      swap32(s, t);
+      float a = fmaxf(s, t);      // [A B C D]
+      float c = a;
+      swap16(a, c);               // [A A C C], [B B D D]
+      float a2 = a, c2 = c;
+      swap32(a, a2);              // [A A A A], [C C C C]
+      swap32(c, c2);              // [B B B B], [D D D D]
+      x[q] = a;
+      x[q + 1] = c;
+      x[q + 2] = a2;
+      x[q + 3] = c2;
+    }
+  }
+}
+
 // Reductions over the wave: inside 16-lane rows with DPP (quad_perm x2, half mirror, mirror), then across rows with
 // the permlane swaps. Every lane ends with the same value.
 __device__ __forceinline__ float wave_max(float x) {
@@ -440,16 +507,19 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
       }
     }
   }
+  // one running max per wave: the rows of a wave can then be merged by plain sums
+  float mt[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float mt = s[g][0];
+    mt[g] = s[g][0];
 #pragma unroll
-    for (int i = 1; i < PPT; ++i) mt = fmaxf(mt, s[g][i]);
-    // one running max per wave: the rows of a wave can then be merged by plain sums
-    if (LPR == 8) mt = fmaxf(mt, lane_xor<8>(mt));
-    mt = fmaxf(mt, lane_xor<16>(mt));
-    mt = fmaxf(mt, lane_xor<32>(mt));
-    const float mn = fmaxf(m[g], mt);
+    for (int i = 1; i < PPT; ++i) mt[g] = fmaxf(mt[g], s[g][i]);
+    if (LPR == 8) mt[g] = fmaxf(mt[g], lane_xor<8>(mt[g]));
+  }
+  rows_max<G>(mt);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mn = fmaxf(m[g], mt[g]);
     const float mu = (mn == -INFINITY) ? 0.f : mn;
     const float alpha = fast_exp2(m[g] - mu);
     l[g] *= alpha;
@@ -472,18 +542,6 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
     }
-  }
-}
-
-// Add lane (lane ^ OFF)'s (l, acc), which covers the same dims for other KV rows under the same wave-uniform max.
-// Both lanes end with the same sums.
-template <int OFF, int G>
-__device__ __forceinline__ void sum_rows(float (&l)[G], float (&acc)[G][8]) {
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] += lane_xor<OFF>(l[g]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] += lane_xor<OFF>(acc[g][j]);
   }
 }
 
@@ -631,25 +689,42 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     }
   }
 
-  // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims)
-  if (LPR == 8) sum_rows<8, G>(l, acc);
-  sum_rows<16, G>(l, acc);
-  sum_rows<32, G>(l, acc);
+  // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims): the G * 8 accumulators and
+  // G sums, zero-padded to NQ groups of four, are summed across rows transposed, so row r of red[q] holds the wave's
+  // total of value 4 q + r (for head_dim 64 the two 8-lane rows of each 16-lane row are added first)
+  constexpr int NV = 9 * G, NQ = (NV + 3) / 4;
+  float flat[4 * NQ];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) flat[8 * g + j] = acc[g][j];
+    flat[8 * G + g] = l[g];
+  }
+#pragma unroll
+  for (int v = NV; v < 4 * NQ; ++v) flat[v] = 0.f;
+  if (LPR == 8) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) flat[v] += lane_xor<8>(flat[v]);
+  }
+  float red[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) red[q] = rows_sum4(flat[4 * q], flat[4 * q + 1], flat[4 * q + 2], flat[4 * q + 3]);
 
   // merge the NW waves through LDS
   __shared__ float s_acc[NW][G][D];
   __shared__ float s_m[NW][G], s_l[NW][G];
-  const int w = tid / kWave, lane = tid % kWave;
-  if (lane < LPR) {
+  const int w = tid / kWave, lane = tid % kWave, row16 = lane / 16;
+  if (lane % 16 < LPR) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_acc[w][g][8 * c + j] = acc[g][j];
-      if (lane == 0) {
-        s_m[w][g] = m[g];
-        s_l[w][g] = l[g];
-      }
+    for (int q = 0; q < NQ; ++q) {
+      const int f = 4 * q + row16;
+      if (f < 8 * G) s_acc[w][f / 8][8 * c + f % 8] = red[q];
+      else if (f < NV && c == 0) s_l[w][f - 8 * G] = red[q];
     }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) s_m[w][g] = m[g];
   }
   __syncthreads();
   (void)RPW;
