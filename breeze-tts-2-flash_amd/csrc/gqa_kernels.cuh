@@ -50,8 +50,8 @@ struct Params {
   int64_t o_sb, o_sh, o_st;
   int B, NH, NKV, cap, splits, min_chunk;
   int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
-  float* part_acc;   // [B * T, NH, splits, D]  unnormalised sum_p 2^(s_p - m) v_p
-  float2* part_ml;   // [B * T, NH, splits]     (m, sum_p 2^(s_p - m))
+  float* part_acc;   // [B * T, NKV, splits, G * D]  unnormalised sum_p 2^(s_p - m) v_p
+  float2* part_ml;   // [B * T, NKV, splits, G]      (m, sum_p 2^(s_p - m))
   int* counters;     // [B * T, NKV] x kCounterStride arrivals, reset by the merging workgroup
   // fused prologue only
   const uint16_t* qkv;  // [B, (NH + 2 NKV) * D] raw projections: q heads | k heads | v heads
@@ -133,26 +133,8 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
-// Value of lane (lane ^ OFF) for OFF in {8, 16, 32}, all on the VALU: row_ror:8 inside each 16-lane row for 8;
-// v_permlane16_swap / v_permlane32_swap for 16 / 32. A swap of x with itself leaves, in one of its two results, this
-// lane's own value and, in the other, the partner's; XOR-ing both with the own bits keeps the partner's bits
-// whichever result holds which.
-template <int OFF>
-__device__ __forceinline__ float lane_xor(float x) {
-  static_assert(OFF == 8 || OFF == 16 || OFF == 32, "lane_xor: 8, 16 or 32");
-  if constexpr (OFF == 8) {
-    return dpp<0x128>(x);
-  } else {
-    const uint32_t u = __float_as_uint(x);
-    if constexpr (OFF == 16) {
-      const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-      return __uint_as_float(r[0] ^ r[1] ^ u);
-    } else {
-      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-      return __uint_as_float(r[0] ^ r[1] ^ u);
-    }
-  }
-}
+// Value of lane (lane ^ 8) inside each 16-lane row: DPP row_ror:8, on the VALU.
+__device__ __forceinline__ float lane_xor8(float x) { return dpp<0x128>(x); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t f = {lo, hi};
@@ -173,7 +155,7 @@ __device__ __forceinline__ void round8(float (&v)[8]) {
 // row; row_ror:8 for head_dim 128, a bpermute for head_dim 64.
 template <int LPR>
 __device__ __forceinline__ float half_partner(float x) {
-  if constexpr (LPR == 16) return lane_xor<8>(x);
+  if constexpr (LPR == 16) return lane_xor8(x);
   else return __shfl_xor(x, LPR / 2);
 }
 
@@ -321,6 +303,15 @@ __device__ __forceinline__ void rows_max(float (&x)[N]) {
   }
 }
 
+// Raw buffer resource (gfx9 V#: base, stride 0, num_records bytes, word 3 = DATA_FORMAT 32) over the bytes [0, bytes)
+// of one (row, kv head) span. A buffer load at an offset >= bytes returns zero and makes no memory access.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ Rsrc span_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRsrcWord3);
+}
+
 // Reductions over the wave: inside 16-lane rows with DPP (quad_perm x2, half mirror, mirror), then across rows with
 // the permlane swaps. Every lane ends with the same value.
 __device__ __forceinline__ float wave_max(float x) {
@@ -328,13 +319,22 @@ __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp<0x4e>(x));
   x = fmaxf(x, dpp<0x141>(x));
   x = fmaxf(x, dpp<0x140>(x));
-  x = fmaxf(x, lane_xor<16>(x));
-  return fmaxf(x, lane_xor<32>(x));
+  float y = x;
+  swap16(x, y);  // [x0 x0 x2 x2], [x1 x1 x3 x3]
+  x = fmaxf(x, y);
+  y = x;
+  swap32(x, y);
+  return fmaxf(x, y);
 }
+// The same order of additions in every lane, so all lanes hold the same bits.
 __device__ __forceinline__ float wave_sum(float x) {
   x = row_sum<16>(x);
-  x += lane_xor<16>(x);
-  return x + lane_xor<32>(x);
+  float y = x;
+  swap16(x, y);
+  x += y;
+  y = x;
+  swap32(x, y);
+  return x + y;
 }
 
 // Split partials cross workgroups (and XCDs, each with its own L2) inside one launch, so they are written and read
@@ -343,24 +343,28 @@ __device__ __forceinline__ float wave_sum(float x) {
 __device__ __forceinline__ void st_agent(float* ptr, float v) {
   __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_agent(const float* ptr) {
-  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
-// Every load the merge needs is issued before anything waits: each thread's first kBatch split partials for its kOut
-// (q head, dim) outputs, and the (max, sum) pairs of q head `wave` (one lane per split). Split weights
-// w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s are reduced over the wave with DPP and lane swaps and stored to LDS
-// zero-padded, so the weighted sum over the first kBatch splits needs no per-split condition.
+// The partials of one (row, kv head) are read through buffer resources cut at nact splits, with the sc1 cache policy
+// (bit 4 of the buffer instruction's cache-policy operand on gfx940 and later: the cache behaviour of an agent-scope
+// relaxed atomic load), so every load is unconditional and splits past nact read 0 without a memory access. All loads
+// are issued before anything waits: each thread's first kBatch partials for its kOut (q head, dim) outputs, and the
+// (max, sum) pairs of q head `wave` (one lane per split). Split weights w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s are
+// reduced over the wave and stored to LDS zero-padded, so the weighted sum needs no per-split condition.
+constexpr int kSc1 = 16;
+
 template <int D, int G, int NT>
 __device__ void merge_splits(const Params& p, int z, int h, int nact) {
-  constexpr int kBatch = 32;
+  constexpr int kBatch = 16;
   constexpr int NW = NT / kWave;
   constexpr int kOut = (G * D + NT - 1) / NT;
   constexpr int kPerLane = kMaxSplits / kWave;
+  constexpr int GD = G * D;
   __shared__ __align__(16) float s_w[G][kMaxSplits];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int64_t row0 = (int64_t)z * p.NH + h * G;  // first q head of the group, as a [B * T * NH] row index
+  const int64_t unit = (int64_t)z * p.NKV + h;
+  const Rsrc racc = span_rsrc(p.part_acc + unit * p.splits * GD, nact * GD * 4);
+  const Rsrc rml = span_rsrc(p.part_ml + unit * p.splits * G, nact * G * 8);
   const int b = z / p.T, tok = z - b * p.T;
   uint16_t* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)tok * p.o_st;
 
@@ -368,20 +372,20 @@ __device__ void merge_splits(const Params& p, int z, int h, int nact) {
 #pragma unroll
   for (int k = 0; k < kOut; ++k) {
     const int o = tid + k * NT;
-    if (o < G * D) {
-      const float* pa = p.part_acc + (row0 + o / D) * p.splits * D + o % D;
+    if (o < GD) {  // uniform over the wave: GD is a multiple of 64
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) t[k][u] = (u < nact) ? ld_agent(pa + (int64_t)u * D) : 0.f;
+      for (int u = 0; u < kBatch; ++u)
+        t[k][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(racc, (u * GD + o) * 4, 0, kSc1));
     }
   }
   float mv[kPerLane], lv[kPerLane];
   auto load_ml = [&](int g) {
-    const float* ml = reinterpret_cast<const float*>(p.part_ml + (row0 + g) * p.splits);
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
-      const int s = lane + kWave * j;
-      mv[j] = (s < nact) ? ld_agent(ml + 2 * s) : -INFINITY;
-      lv[j] = (s < nact) ? ld_agent(ml + 2 * s + 1) : 0.f;
+      const int sp = lane + kWave * j;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rml, (sp * G + g) * 8, 0, kSc1);
+      mv[j] = sp < nact ? __uint_as_float(v[0]) : -INFINITY;
+      lv[j] = __uint_as_float(v[1]);  // 0 past nact
     }
   };
   if (wave < G) load_ml(wave);
@@ -409,20 +413,20 @@ __device__ void merge_splits(const Params& p, int z, int h, int nact) {
 #pragma unroll
   for (int k = 0; k < kOut; ++k) {
     const int o = tid + k * NT;
-    if (o >= G * D) continue;
-    const int g = o / D, d = o % D;
-    const float* pa = p.part_acc + (row0 + g) * p.splits * D + d;
+    if (o >= GD) continue;
+    const int g = o / D;
     float a = 0.f;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][u], t[k][u], a);
     for (int s0 = kBatch; s0 < nact; s0 += kBatch) {
       float x[kBatch];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) x[u] = (s0 + u < nact) ? ld_agent(pa + (int64_t)(s0 + u) * D) : 0.f;
+      for (int u = 0; u < kBatch; ++u)
+        x[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(racc, ((s0 + u) * GD + o) * 4, 0, kSc1));
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) a = fmaf(s_w[g][s0 + u], x[u], a);
     }
-    orow[(int64_t)(h * G + g) * p.o_sh + d] = f32_to_bf16(a);
+    orow[(int64_t)(h * G + g) * p.o_sh + o % D] = f32_to_bf16(a);
   }
 }
 
@@ -432,15 +436,6 @@ struct Tile {
   uint4 k[PPT], v[PPT];
   float m[PPT];
 };
-
-// Raw buffer resource (gfx9 V#: base, stride 0, num_records bytes, word 3 = DATA_FORMAT 32) over the bytes [0, bytes)
-// of one (row, kv head) span. A buffer load at an offset >= bytes returns zero and makes no memory access.
-using Rsrc = __amdgpu_buffer_rsrc_t;
-constexpr int kRsrcWord3 = 0x00020000;
-
-__device__ __forceinline__ Rsrc span_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRsrcWord3);
-}
 
 // The K, V (and mask) spans of one (row, kv head), each cut at position hi: positions >= hi are outside the resource,
 // so their loads return zero without reading memory (NaN tails and slots past the row stay unread).
@@ -514,7 +509,7 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
     mt[g] = s[g][0];
 #pragma unroll
     for (int i = 1; i < PPT; ++i) mt[g] = fmaxf(mt[g], s[g][i]);
-    if (LPR == 8) mt[g] = fmaxf(mt[g], lane_xor<8>(mt[g]));
+    if (LPR == 8) mt[g] = fmaxf(mt[g], lane_xor8(mt[g]));
   }
   rows_max<G>(mt);
 #pragma unroll
@@ -704,7 +699,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   for (int v = NV; v < 4 * NQ; ++v) flat[v] = 0.f;
   if (LPR == 8) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) flat[v] += lane_xor<8>(flat[v]);
+    for (int v = 0; v < NV; ++v) flat[v] += lane_xor8(flat[v]);
   }
   float red[NQ];
 #pragma unroll
@@ -746,11 +741,11 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
       p.out[(int64_t)b * p.o_sb + (int64_t)tok * p.o_st + (int64_t)hq * p.o_sh + d] =
           f32_to_bf16(L > 0.f ? A / L : 0.f);
     } else {
-      const int64_t ps = ((int64_t)z * p.NH + hq) * p.splits + split;
-      st_agent(p.part_acc + ps * D + d, A);
+      const int64_t ps = ((int64_t)z * p.NKV + h) * p.splits + split;  // this split of this (row, kv head)
+      st_agent(p.part_acc + ps * (G * D) + o, A);
       if (d == 0) {
-        st_agent(reinterpret_cast<float*>(p.part_ml + ps), M);
-        st_agent(reinterpret_cast<float*>(p.part_ml + ps) + 1, L);
+        st_agent(reinterpret_cast<float*>(p.part_ml + ps * G + g), M);
+        st_agent(reinterpret_cast<float*>(p.part_ml + ps * G + g) + 1, L);
       }
     }
   }
