@@ -233,6 +233,9 @@ int check_common(const bz_gqa_decode_args* a, bool need_q) {
   if (rc != BZ_OK) return rc;
   const uintptr_t kp = reinterpret_cast<uintptr_t>(a->k_cache), vp = reinterpret_cast<uintptr_t>(a->v_cache);
   if ((kp | vp) & 15) return BZ_ERR_ALIGNMENT;
+  if (need_q && ((reinterpret_cast<uintptr_t>(a->q) & 15) || ((a->q_stride_b | a->q_stride_h) & 7) ||
+                 (tokens_of(a) > 1 && (a->q_stride_t & 7))))
+    return BZ_ERR_ALIGNMENT;
   if ((a->kv_stride_b | a->kv_stride_h | a->kv_stride_s) & 7) return BZ_ERR_ALIGNMENT;
   if (a->kv_stride_s < a->head_dim) return BZ_ERR_SHAPE;
   if (a->tokens_per_row < 0 || (int64_t)a->batch * tokens_of(a) > 65535) return BZ_ERR_SHAPE;  // grid.z limit

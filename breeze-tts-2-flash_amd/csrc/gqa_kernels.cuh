@@ -563,7 +563,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   constexpr int NS = (NE + RPW - 1) / RPW;
   static_assert(!FUSED || D == 128, "the fused prologue is built for head_dim 128");
   const int rw = (tid % kWave) / LPR;  // row inside the wave
-  uint16_t qh[G][8];
+  uint4 qr[G];
   uint4 xe[NS], we[NS], xv, rc, rs;
   int64_t newpos64 = -1;
   if (FUSED) {
@@ -583,8 +583,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const uint16_t* qsrc = p.q + (int64_t)b * p.q_sb + (int64_t)tok * p.q_st + (int64_t)(h * G + g) * p.q_sh + 8 * c;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qh[g][j] = qsrc[j];
+      qr[g] = *reinterpret_cast<const uint4*>(qsrc);  // 16-byte aligned: the host checks q and its strides
     }
   }
 
@@ -652,12 +651,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     }
   } else {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      qp[g].x = qh[g][0] | ((uint32_t)qh[g][1] << 16);
-      qp[g].y = qh[g][2] | ((uint32_t)qh[g][3] << 16);
-      qp[g].z = qh[g][4] | ((uint32_t)qh[g][5] << 16);
-      qp[g].w = qh[g][6] | ((uint32_t)qh[g][7] << 16);
-    }
+    for (int g = 0; g < G; ++g) qp[g] = qr[g];
   }
 
   float m[G], l[G], acc[G][8];

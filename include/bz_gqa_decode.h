@@ -59,7 +59,8 @@ typedef enum bz_combine_mode {
 
 /* Arguments of bz_gqa_decode (the reference op's (q, k_cache, v_cache, seq_lens, scale) -> out). */
 typedef struct bz_gqa_decode_args {
-  /* query [batch, num_q_heads, head_dim] bf16: element (b, h, d) at q[b*q_stride_b + h*q_stride_h + d] */
+  /* query [batch, num_q_heads, head_dim] bf16: element (b, h, d) at q[b*q_stride_b + h*q_stride_h + d]; q and its
+     strides 16-byte aligned (multiples of 8 elements) */
   const void* q;
   int64_t q_stride_b, q_stride_h;
   /* KV cache [batch, num_kv_heads, capacity, head_dim] bf16 (transformers StaticCache layer layout). K and V

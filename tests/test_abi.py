@@ -113,6 +113,8 @@ def _good_args(K, **over):
     (dict(num_kv_heads=3), -2), (dict(batch=0), -2), (dict(capacity=0), -2), (dict(kv_stride_s=64), -2),
     (dict(head_dim=96), -3), (dict(num_q_heads=24, num_kv_heads=8), -3), (dict(num_q_heads=32, num_kv_heads=2), -3),
     (dict(k_cache=0x100008), -4), (dict(kv_stride_s=132), -4), (dict(kv_stride_h=256 * 128 + 4), -4),
+    (dict(q=0x10004), -4), (dict(q_stride_h=132), -4), (dict(q_stride_b=16 * 128 + 2), -4),
+    (dict(tokens_per_row=2, q_stride_t=68), -4), (dict(tokens_per_row=1, q_stride_t=68), -5),
     (dict(mask=0x50000, mask_dtype=0), -6), (dict(mask_dtype=7), -6),
     (dict(num_splits=-1), -2), (dict(num_splits=257), -2),
     (dict(combine=3), -9),
