@@ -445,6 +445,10 @@ struct Spans {
   uint32_t lane_off;   // this lane's 16 bytes inside a row
 };
 
+// K and V are read once per call: their loads carry the nt (non-temporal, bit 1 of the cache-policy operand) hint so
+// the streamed bytes do not push the small hot data (lengths, q, the split workspace) out of the L2.
+constexpr int kStream = 2;
+
 // Issue every K and V load of a tile (and its mask values) before any arithmetic. The loads are unconditional (the
 // resource bounds do the cut at hi), so the compiler's vmcnt accounting stays exact and earlier loads (q, the fused
 // prologue's inputs) can be consumed while the tile is still in flight.
@@ -454,8 +458,8 @@ __device__ __forceinline__ void load_tile(Tile<PPT>& t, const Spans& sp, int pos
   for (int i = 0; i < PPT; ++i) {
     const uint32_t pos = (uint32_t)(pos0 + ROWS * i);
     const uint32_t off = pos * sp.row_bytes + sp.lane_off;
-    t.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sp.k, off, 0, 0));
-    t.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sp.v, off, 0, 0));
+    t.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sp.k, off, 0, kStream));
+    t.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sp.v, off, 0, kStream));
     if (MK == BZ_MASK_BF16) t.m[i] = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(sp.m, pos * 2, 0, 0));
     if (MK == BZ_MASK_F32)
       t.m[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sp.m, pos * 4, 0, 0));
