@@ -612,14 +612,13 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     if (MK == BZ_MASK_F32) sp.m = span_rsrc(static_cast<const float*>(p.mask) + (int64_t)b * p.m_sb, 4 * hi);
   }
 
-  // The first tile's K/V loads (and, for PPT <= 4, the second's) go out before q is converted, so no wave waits on
+  // The first two tiles' K/V loads go out before q is converted, so no wave waits on
   // q before streaming. Tiles A and B ping-pong without register copies: while one is consumed the other's loads
   // are in flight. Loads of positions >= hi fall outside the spans and make no memory access, so a one-tile chunk
   // issues no extra traffic.
-  constexpr bool kPingPong = PPT <= 4;
   Tile<PPT> ta, tb;
   load_tile<ROWS, PPT, MK>(ta, sp, lo + r);
-  if (kPingPong) load_tile<ROWS, PPT, MK>(tb, sp, lo + TP + r);
+  load_tile<ROWS, PPT, MK>(tb, sp, lo + TP + r);
   // keep the machine scheduler from sinking the tile loads below the q / prologue arithmetic (which would make that
   // arithmetic wait for its own inputs before any K/V load is in flight)
   __builtin_amdgcn_sched_barrier(0);
@@ -667,19 +666,12 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
   }
 
-  if (kPingPong) {
-    for (int t0 = lo; t0 < hi; t0 += 2 * TP) {
-      consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
-      if (t0 + TP >= hi) break;
-      load_tile<ROWS, PPT, MK>(ta, sp, t0 + 2 * TP + r);
-      consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(tb, qp, p.scale_log2, m, l, acc, t0 + TP + r, hi, newpos, knew, vnew);
-      load_tile<ROWS, PPT, MK>(tb, sp, t0 + 3 * TP + r);
-    }
-  } else {
-    for (int t0 = lo; t0 < hi; t0 += TP) {
-      consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
-      if (t0 + TP < hi) load_tile<ROWS, PPT, MK>(ta, sp, t0 + TP + r);
-    }
+  for (int t0 = lo; t0 < hi; t0 += 2 * TP) {
+    consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(ta, qp, p.scale_log2, m, l, acc, t0 + r, hi, newpos, knew, vnew);
+    if (t0 + TP >= hi) break;
+    load_tile<ROWS, PPT, MK>(ta, sp, t0 + 2 * TP + r);
+    consume_tile<LPR, ROWS, G, PPT, MK, FUSED>(tb, qp, p.scale_log2, m, l, acc, t0 + TP + r, hi, newpos, knew, vnew);
+    load_tile<ROWS, PPT, MK>(tb, sp, t0 + 3 * TP + r);
   }
 
   // merge the RPW rows of each wave (lanes c, c + LPR, c + 2 LPR, ... hold the same dims): the G * 8 accumulators and
@@ -819,8 +811,7 @@ template <int D, int G, int MK, int NT, bool FUSED>
 SplitFn pick_ppt(int ppt) {
   switch (ppt) {
     case 1: return gqa_split_kernel<D, G, 1, MK, NT, FUSED>;
-    case 2: return gqa_split_kernel<D, G, 2, MK, NT, FUSED>;
-    default: return gqa_split_kernel<D, G, 4, MK, NT, FUSED>;
+    default: return gqa_split_kernel<D, G, 2, MK, NT, FUSED>;
   }
 }
 
