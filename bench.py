@@ -176,24 +176,33 @@ def time_depth_frame(pkg, dev, steps, warmup):
     return us_frame, frame_bytes
 
 
-def cpu_baseline(w, calls=200, warmup=20):
-    """The reference's eager CPU attention on workload w (its StaticCache capacity plus the interval mask, as the
-    reference runs decode), median of `calls` after `warmup`."""
+def cpu_baseline(w, calls=200, warmup=20, kind="eager", budget_s=10.0):
+    """Median µs per call on the host of the reference's CPU attention for workload w. kind "eager": the eager chain
+    (repeat_kv + bf16 matmul + fp32 softmax + matmul, oracle/attention.py:eager_bf16) over the StaticCache capacity with
+    the interval mask, as the reference runs decode; kind "sdpa": torch's fp32 scaled_dot_product_attention per row
+    over the valid range (oracle/attention.py:sdpa_fp32, the north-star oracle). At most `calls` calls or
+    `budget_s` seconds after `warmup`."""
     import torch
-    from oracle.attention import eager_bf16, interval_mask
+    from oracle.attention import eager_bf16, interval_mask, sdpa_fp32
 
     threads = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
-    q = w.q[:, :, None, :]
-    L = int(w.seq_lens[0])
-    mask = interval_mask([0] * w.batch, L - 1, w.capacity)
+    if kind == "eager":
+        q = w.q[:, :, None, :]
+        mask = interval_mask([0] * w.batch, int(w.seq_lens[0]) - 1, w.capacity)
+
+        def run():
+            eager_bf16(q, w.k, w.v, mask, w.scale)
+    else:
+        def run():
+            sdpa_fp32(w.q, w.k, w.v, w.seq_lens.tolist(), w.scale)
     for _ in range(warmup):
-        eager_bf16(q, w.k, w.v, mask, w.scale)
+        run()
     ts = []
-    t_end = time.perf_counter() + 30.0
+    t_end = time.perf_counter() + budget_s
     for _ in range(calls):
         t0 = time.perf_counter_ns()
-        eager_bf16(q, w.k, w.v, mask, w.scale)
+        run()
         ts.append(time.perf_counter_ns() - t0)
         if time.perf_counter() > t_end:
             break
@@ -315,13 +324,21 @@ def main():
         print(f"[bench] config 5 depth frame: {us_f:.3f} us/frame", file=sys.stderr, flush=True)
         line["extra"] = extra
     if not args.no_cpu:
-        us_cpu, cores, n = cpu_baseline(w2)
+        us_cpu, cores, n = cpu_baseline(w2, budget_s=30.0)
         line["cpu_baseline"] = {"value": round(nbytes / us_cpu / 1e3, 3), "unit": "GB/s", "cores": cores,
                                 "kind": "port", "us_per_call": round(us_cpu, 1),
                                 "sample": f"config {cfg} inputs, the reference's eager bf16 chain over the full "
                                           f"{w2.capacity}-slot cache with the interval mask, median of {n} calls "
                                           f"after 20 warmups"}
         print(f"[bench] cpu baseline: {us_cpu:.1f} us/call on {cores} threads", file=sys.stderr, flush=True)
+        # beside it: the reference's own CPU-runnable case (config 1) and the fp32 SDPA oracle on the headline inputs
+        us_c1, _, n1 = cpu_baseline(workloads.make(1), kind="eager", budget_s=5.0)
+        us_sd, _, nsd = cpu_baseline(w2, kind="sdpa", calls=50, warmup=5, budget_s=5.0)
+        line["cpu_baseline"]["extra"] = {
+            "config1_eager_us_per_call": round(us_c1, 1), "config1_calls": n1,
+            f"config{cfg}_sdpa_fp32_us_per_call": round(us_sd, 1), f"config{cfg}_sdpa_calls": nsd}
+        print(f"[bench] cpu config 1 eager: {us_c1:.1f} us/call; config {cfg} sdpa fp32: {us_sd:.1f} us/call",
+              file=sys.stderr, flush=True)
     print(json.dumps(line), flush=True)
 
 

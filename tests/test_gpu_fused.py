@@ -160,3 +160,23 @@ def test_fused_decode_loop_in_hip_graph(device):
         assert np.array_equal(got_v[:, :, pos], ref_v2[:, :, pos])
         # carry the GPU's own cache forward so that later steps compare like with like
         ref_k, ref_v = got_k, got_v
+
+
+def test_golden_fused_fixtures(device):
+    """tests/golden/fused_and_tokens.npz: the fused cases through gqa_decode_fused."""
+    from tests.golden.make_golden import OUT2, load
+
+    for name, c in sorted(load(OUT2).items()):
+        if not name.startswith("fused"):
+            continue
+        pos = int(c["pos"])
+        kc, vc = tens(c["k"], device), tens(c["v"], device)
+        out = gqa_decode_fused(tens(c["qkv"], device), tens(c["qn"], device), tens(c["kn"], device), float(c["eps"]),
+                               tens(c["cos"], device), tens(c["sin"], device), kc, vc,
+                               torch.tensor([pos], dtype=torch.int64, device=device), float(c["scale"]),
+                               seq_lens=torch.from_numpy(c["lens"]).to(device),
+                               kv_start=torch.from_numpy(c["starts"]).to(device))
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), c["out"], f"golden {name}")
+        assert_k_slot(bits(kc)[:, :, pos], c["k_slot"], f"golden {name}")
+        assert np.array_equal(bits(vc)[:, :, pos], c["v_slot"]), f"golden {name}: v slot"

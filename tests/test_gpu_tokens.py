@@ -88,3 +88,19 @@ def test_rows_shorter_than_tokens(device):
     torch.cuda.synchronize()
     check(out, q, k, v, [1, 2], D ** -0.5, what="short rows")
     assert torch.count_nonzero(out[0, :2]) == 0 and torch.count_nonzero(out[1, 0]) == 0
+
+
+def test_golden_tokens_fixtures(device):
+    """tests/golden/fused_and_tokens.npz: the several-token cases through gqa_decode."""
+    from tests.golden.make_golden import OUT2, load
+
+    for name, c in sorted(load(OUT2).items()):
+        if not name.startswith("tokens"):
+            continue
+        t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)  # noqa: E731
+        out = gqa_decode(t(c["q"]), t(c["k"]), t(c["v"]), torch.from_numpy(c["lens"]).to(device), float(c["scale"]),
+                         kv_start=torch.from_numpy(c["starts"]).to(device))
+        torch.cuda.synchronize()
+        g = out.float().cpu().numpy()
+        excess = np.abs(g - c["out"]) - (2e-3 + 1e-2 * np.abs(c["out"]))
+        assert excess.max() <= 0, f"golden {name}: excess {excess.max():.3e}"
