@@ -51,8 +51,12 @@ def default_splits(batch: int, num_kv_heads: int, head_dim: int, capacity: int, 
 
 def get_workspace(device: torch.device, batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
                   capacity: int, num_splits: int = 0, max_seq_len: int = 0) -> torch.Tensor:
-    """Zero-initialised, cached scratch for these sizes (the library keeps it zero-ready between calls)."""
-    key = (str(device), batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
+    """Zero-initialised, cached scratch for these sizes on the device's current stream (the library keeps it
+    zero-ready between calls). One per stream: calls in flight on two streams must not share the split counters and
+    partials. The first call on a stream that is being captured into a HIP graph allocates it from the graph's pool
+    (its zero fill is then replayed with the graph); an eager call on the capture stream beforehand avoids that."""
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (str(device), stream, batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
     with _WS_LOCK:
         ws = _WS.get(key)
         if ws is None:

@@ -362,3 +362,36 @@ def test_golden_fixtures(device):
             out2 = gqa_decode_masked(q, k, v, mask, float(c["scale"]))
             torch.cuda.synchronize()
             assert_close(out2.float().cpu(), c["out"], f"golden {name} (masked entry)")
+
+
+def test_concurrent_streams_and_threads(device):
+    """Two host threads, each on its own stream with the default (per-stream) workspace, run decode calls at the same
+    time on different data; every output matches the oracle (the op is stateless; the split counters and partials
+    are per stream)."""
+    import threading
+
+    cases = [rand_case(60 + i, 2, 16, 8, 128, 2048, [1500 - 300 * i, 900 + 100 * i]) for i in range(2)]
+    outs = [None, None]
+    errors = []
+
+    def worker(i):
+        try:
+            w, _ = cases[i]
+            s = torch.cuda.Stream(device=device)
+            with torch.cuda.stream(s):
+                g = w.to(device)
+                for _ in range(50):
+                    o = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale)
+                s.synchronize()
+                outs[i] = o.float().cpu()
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for i in range(2):
+        assert_close(outs[i], oracle(cases[i][0]), f"stream {i}")
