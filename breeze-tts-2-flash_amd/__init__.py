@@ -6,13 +6,16 @@ Public API:
   gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, ...)
   attn_decode(query, kc, vc, mask, scaling, scores, cmax, part, counters, out, dbg=None)   (reference order)
   attn_decode_fused(qkv, qn_w, kn_w, eps, cos, sin, kc, vc, mask, cache_pos, scaling, ..., out, dbg=None)
-  build() / load()   compile / open libbz_gqa_decode.so (C ABI: include/bz_gqa_decode.h)
+  gemv_seg / gemv_resid / gemv_gateup / rmsnorm   backbone decode GEMVs (reference order; C ABI include/bz_gemv.h)
+  build() / load()   compile / open libbz_gqa_decode.so (C ABI: include/bz_gqa_decode.h, include/bz_gemv.h)
 """
 from .attention import (default_splits, get_workspace, gqa_decode, gqa_decode_fused, gqa_decode_masked,
                         workspace_bytes)
 from .compat import attn_decode, attn_decode_fused
+from .gemv import gemv_gateup, gemv_resid, gemv_seg, rmsnorm
 from .kernels import build, load
 from . import hf_attention
 
 __all__ = ["gqa_decode", "gqa_decode_masked", "gqa_decode_fused", "attn_decode", "attn_decode_fused",
+           "gemv_seg", "gemv_resid", "gemv_gateup", "rmsnorm",
            "workspace_bytes", "default_splits", "get_workspace", "build", "load"]

@@ -1,0 +1,365 @@
+// Backbone decode GEMVs for gfx950 (include/bz_gemv.h): the reference's flash_bb_fused (flash/csrc/bb_fused.cu).
+//
+// y[m, n] = epilogue(sum_k xin[m, k] * W[n, k]) for the decode step's M <= 4 rows: weight-streaming and HBM-bound
+// (each weight byte is used M times, 2 FLOPs each). The work is laid out for the weights:
+//   - a wave owns R output rows (2 R weight rows for the SiLU * up epilogue: gate and up of the same outputs) and
+//     streams them whole; lane l reads the 16 bytes at k = 8 l + 512 c of every chunk c, so one wave load instruction
+//     covers 1 KiB of one weight row. Rows are raw buffer resources cut at k (and empty past the last output row), so
+//     every load is unconditional, nothing past a row is read, and the compiler's vmcnt accounting stays exact.
+//   - two tiles of R x U chunks are in flight (ping-pong); the first two are issued before the x prologue.
+//   - x (RMSNorm'ed at the eager rounding points when asked) is staged once per workgroup in LDS, zero-padded to a
+//     multiple of the tile, and read with one ds_read_b128 per chunk and row of x.
+//   - products: four v_dot2c_f32_bf16 per 16 bytes (bf16 x bf16 exact, fp32 accumulation); the R * M (2 R * M)
+//     accumulators are summed over the wave with DPP inside 16-lane rows and transposed permlane swaps across rows,
+//     so each lane of a row ends with one finished output, written with the epilogue by that row's first lane.
+// The weight loads carry the non-temporal hint: 2.8 GB of weights stream through per decode step.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "bz_gemv.h"
+#include "device_common.cuh"
+
+namespace {
+
+constexpr int kGemvThreads = 256;              // 4 waves per workgroup
+constexpr int kGemvWaves = kGemvThreads / kWave;
+constexpr int kChunk = 8 * kWave;              // k elements per wave load instruction
+constexpr int kU = 2;                          // chunks per tile
+constexpr int kTileK = kChunk * kU;            // k elements per tile
+constexpr int kMaxLds = 64 * 1024;             // bytes of LDS for x
+
+struct GemvParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* nw;
+  float eps;
+  const uint16_t* w0;
+  const uint16_t* w1;
+  const uint16_t* w2;
+  int n0, n1, ntot;  // rows of segments 0 and 1; output rows
+  int k, kp;         // k, and k rounded up to kTileK (the LDS row pitch of x)
+  uint16_t* y;
+  int64_t ldy;
+  const uint16_t* res;
+  int64_t ldr;
+};
+
+// Stage x (m rows of k, zero-padded to kp) into LDS; with NORM, as bf16(w * bf16(x * rsqrt(mean(x^2) + eps))) with
+// the mean over the k real elements (bb_fused.cu:95-140).
+template <int M, bool NORM>
+__device__ __forceinline__ void stage_x(const GemvParams& p, uint16_t* xs) {
+  const int tid = threadIdx.x;
+  const int kv = p.kp / 8;  // 16-byte vectors per LDS row
+  float ss[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    ss[m] = 0.f;
+    const Rsrc rx = span_rsrc(p.x + (int64_t)m * p.ldx, p.k * 2);
+    for (int j = tid; j < kv; j += kGemvThreads) {
+      const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, j * 16, 0, 0));
+      reinterpret_cast<uint4*>(xs + m * p.kp)[j] = v;
+      if (NORM) {
+        float f[8];
+        unpack8(v, f);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) ss[m] = fmaf(f[t], f[t], ss[m]);
+      }
+    }
+  }
+  if (!NORM) return;
+  __shared__ float red[kGemvWaves][M];
+  const int lane = tid % kWave, wave = tid / kWave;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float s = wave_sum(ss[m]);
+    if (lane == 0) red[wave][m] = s;
+  }
+  __syncthreads();
+  const Rsrc rw = span_rsrc(p.nw, p.k * 2);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGemvWaves; ++w) tot += red[w][m];
+    const float r = rsqrtf(tot * (1.f / (float)p.k) + p.eps);
+    for (int j = tid; j < kv; j += kGemvThreads) {
+      float f[8], w[8];
+      unpack8(reinterpret_cast<const uint4*>(xs + m * p.kp)[j], f);
+      unpack8(__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, j * 16, 0, 0)), w);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) f[t] *= r;
+      round8(f);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) f[t] *= w[t];
+      reinterpret_cast<uint4*>(xs + m * p.kp)[j] =
+          make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+    }
+  }
+}
+
+template <int M, int R, bool NORM, int EPI>
+__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) {
+  constexpr int NR = EPI == BZ_GEMV_SILU_MUL ? 2 * R : R;  // weight rows per wave
+  extern __shared__ __align__(16) uint16_t xs[];            // [M][kp] bf16
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+
+  // this wave's weight rows (a row past the last output: an empty resource, whose loads read 0)
+  Rsrc wr[NR];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = row0 + r;
+    const int bytes = n < p.ntot ? p.k * 2 : 0;
+    if (EPI == BZ_GEMV_SILU_MUL) {
+      wr[r] = span_rsrc(p.w0 + (int64_t)n * p.k, bytes);
+      wr[R + r] = span_rsrc(p.w1 + (int64_t)n * p.k, bytes);
+    } else {
+      const uint16_t* base = n < p.n0 ? p.w0 + (int64_t)n * p.k
+                           : n < p.n0 + p.n1 ? p.w1 + (int64_t)(n - p.n0) * p.k
+                                             : p.w2 + (int64_t)(n - p.n0 - p.n1) * p.k;
+      wr[r] = span_rsrc(base, bytes);
+    }
+  }
+
+  uint4 ta[NR][kU], tb[NR][kU];
+  const uint32_t lane_off = lane * 16;
+  auto load = [&](uint4 (&t)[NR][kU], int it) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint32_t off = (uint32_t)(it * kTileK + u * kChunk) * 2 + lane_off;
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+        t[r][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr[r], off, 0, kStream));
+    }
+  };
+  // the first two weight tiles do not depend on x: issue them before the prologue
+  load(ta, 0);
+  load(tb, 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  stage_x<M, NORM>(p, xs);
+  __syncthreads();
+
+  float acc[NR][M];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+  auto consume = [&](const uint4 (&t)[NR][kU], int it) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kk = it * kTileK + u * kChunk + lane * 8;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xs + m * p.kp + kk);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float a = acc[r][m];
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
+          acc[r][m] = a;
+        }
+      }
+    }
+  };
+  const int nit = p.kp / kTileK;
+  for (int it = 0; it < nit; it += 2) {
+    consume(ta, it);
+    load(ta, it + 2);  // past k: reads 0 without a memory access
+    if (it + 1 < nit) consume(tb, it + 1);
+    load(tb, it + 3);
+  }
+
+  // sum the accumulators over the wave: DPP inside each 16-lane row, then transposed swaps across the 4 rows, so
+  // row q of red[g] holds the total of flat value 4 g + q. Flat order: (r, m) -> r * M + m for the R output rows,
+  // padded to a multiple of 4 (NG); the up rows of SILU_MUL follow at NG + r * M + m, in the same row as their gate.
+  constexpr int NG = (R * M + 3) / 4 * 4;
+  constexpr int NV = EPI == BZ_GEMV_SILU_MUL ? 2 * NG : NG;
+  float flat[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) flat[v] = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      flat[r * M + m] = row_sum<16>(acc[r][m]);
+      if (EPI == BZ_GEMV_SILU_MUL) flat[NG + r * M + m] = row_sum<16>(acc[R + r][m]);
+    }
+  float red[NV / 4];
+#pragma unroll
+  for (int g = 0; g < NV / 4; ++g) red[g] = rows_sum4(flat[4 * g], flat[4 * g + 1], flat[4 * g + 2], flat[4 * g + 3]);
+
+  if (lane % 16 != 0) return;
+  const int q = lane / 16;
+#pragma unroll
+  for (int g = 0; g < NG / 4; ++g) {
+    const int f = 4 * g + q;
+    if (f >= R * M) continue;
+    const int r = f / M, m = f % M, n = row0 + r;
+    if (n >= p.ntot) continue;
+    float v;
+    if (EPI == BZ_GEMV_PLAIN) {
+      v = red[g];
+    } else if (EPI == BZ_GEMV_RESIDUAL) {
+      v = bf16_to_f32(p.res[(int64_t)m * p.ldr + n]) + bf16_to_f32(f32_to_bf16(red[g]));
+    } else {
+      const float gt = bf16_to_f32(f32_to_bf16(red[g]));
+      const float up = bf16_to_f32(f32_to_bf16(red[NG / 4 + g]));
+      v = bf16_to_f32(f32_to_bf16(gt / (1.f + expf(-gt)))) * up;
+    }
+    p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(v);
+  }
+}
+
+// Standalone row RMSNorm, one workgroup per row (bb_fused.cu:219-248).
+__global__ void __launch_bounds__(kGemvThreads) rmsnorm_kernel(const uint16_t* x, int64_t ldx, const uint16_t* w,
+                                                               float eps, uint16_t* y, int64_t ldy, int k) {
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const uint16_t* xr = x + (int64_t)m * ldx;
+  float ss = 0.f;
+  for (int j = tid * 8; j < k; j += kGemvThreads * 8) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(xr + j), f);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ss = fmaf(f[t], f[t], ss);
+  }
+  __shared__ float red[kGemvWaves];
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kGemvWaves; ++i) tot += red[i];
+  const float r = rsqrtf(tot * (1.f / (float)k) + eps);
+  for (int j = tid * 8; j < k; j += kGemvThreads * 8) {
+    float f[8], ww[8];
+    unpack8(*reinterpret_cast<const uint4*>(xr + j), f);
+    unpack8(*reinterpret_cast<const uint4*>(w + j), ww);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) f[t] *= r;
+    round8(f);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) f[t] *= ww[t];
+    *reinterpret_cast<uint4*>(y + (int64_t)m * ldy + j) =
+        make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- host side
+
+using GemvFn = void (*)(const GemvParams);
+
+template <int M, int R>
+GemvFn pick_epi(int epi, bool norm) {
+  if (epi == BZ_GEMV_PLAIN) return norm ? gemv_kernel<M, R, true, BZ_GEMV_PLAIN> : gemv_kernel<M, R, false, BZ_GEMV_PLAIN>;
+  if (epi == BZ_GEMV_RESIDUAL) return norm ? nullptr : gemv_kernel<M, R, false, BZ_GEMV_RESIDUAL>;
+  if (epi == BZ_GEMV_SILU_MUL)
+    return norm ? gemv_kernel<M, R, true, BZ_GEMV_SILU_MUL> : gemv_kernel<M, R, false, BZ_GEMV_SILU_MUL>;
+  return nullptr;
+}
+
+template <int M>
+GemvFn pick_r(int r, int epi, bool norm) {
+  switch (r) {
+    case 1: return pick_epi<M, 1>(epi, norm);
+    case 2: return pick_epi<M, 2>(epi, norm);
+    default: return pick_epi<M, 4>(epi, norm);
+  }
+}
+
+GemvFn pick_gemv(int m, int r, int epi, bool norm) {
+  switch (m) {
+    case 1: return pick_r<1>(r, epi, norm);
+    case 2: return pick_r<2>(r, epi, norm);
+    case 3: return pick_r<3>(r, epi, norm);
+    case 4: return pick_r<4>(r, epi, norm);
+    default: return nullptr;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Output rows per wave: enough waves to keep every CU's SIMDs streaming (about 8 waves per CU or more).
+int rows_per_wave(int ntot, int epi) {
+  const int rows = epi == BZ_GEMV_SILU_MUL ? 2 * ntot : ntot;
+  if (rows >= 16384) return 4;
+  if (rows >= 8192) return 2;
+  return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStream_t stream) {
+  if (a == nullptr || a->x == nullptr || a->y == nullptr || a->w[0] == nullptr) return BZ_ERR_NULL;
+  if (a->m < 1 || a->m > 4 || a->k <= 0 || (a->k & 7)) return BZ_ERR_SHAPE;
+  if (a->epilogue < BZ_GEMV_PLAIN || a->epilogue > BZ_GEMV_SILU_MUL) return BZ_ERR_UNSUPPORTED;
+  for (int i = 0; i < 3; ++i)
+    if (a->n[i] < 0) return BZ_ERR_SHAPE;
+  int ntot;
+  if (a->epilogue == BZ_GEMV_SILU_MUL) {
+    if (a->w[1] == nullptr) return BZ_ERR_NULL;
+    if (a->n[0] != a->n[1] || a->n[2] != 0) return BZ_ERR_SHAPE;
+    ntot = a->n[0];
+  } else {
+    if ((a->n[1] > 0 && a->w[1] == nullptr) || (a->n[2] > 0 && a->w[2] == nullptr)) return BZ_ERR_NULL;
+    if ((int64_t)a->n[0] + a->n[1] + a->n[2] > INT32_MAX) return BZ_ERR_SHAPE;
+    ntot = a->n[0] + a->n[1] + a->n[2];
+  }
+  if (ntot <= 0) return BZ_ERR_SHAPE;
+  if (a->epilogue == BZ_GEMV_RESIDUAL) {
+    if (a->res == nullptr) return BZ_ERR_NULL;
+    if (a->norm_weight != nullptr) return BZ_ERR_UNSUPPORTED;  // the reference's gemv_resid takes no norm
+  }
+  if (a->x_stride < a->k || a->y_stride < ntot || (a->epilogue == BZ_GEMV_RESIDUAL && a->res_stride < ntot))
+    return BZ_ERR_SHAPE;
+  if (!aligned16(a->x) || (a->x_stride & 7) || (a->norm_weight && !aligned16(a->norm_weight))) return BZ_ERR_ALIGNMENT;
+  for (int i = 0; i < 3; ++i)
+    if (a->w[i] && !aligned16(a->w[i])) return BZ_ERR_ALIGNMENT;
+  const int kp = (a->k + kTileK - 1) / kTileK * kTileK;
+  const size_t lds = (size_t)a->m * kp * 2;
+  if (lds > (size_t)kMaxLds || (int64_t)a->k * 2 > INT32_MAX) return BZ_ERR_UNSUPPORTED;
+
+  const int r = rows_per_wave(ntot, a->epilogue);
+  GemvFn fn = pick_gemv(a->m, r, a->epilogue, a->norm_weight != nullptr);
+  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
+  GemvParams p;
+  p.x = static_cast<const uint16_t*>(a->x);
+  p.ldx = a->x_stride;
+  p.nw = static_cast<const uint16_t*>(a->norm_weight);
+  p.eps = a->eps;
+  p.w0 = static_cast<const uint16_t*>(a->w[0]);
+  p.w1 = static_cast<const uint16_t*>(a->w[1] ? a->w[1] : a->w[0]);
+  p.w2 = static_cast<const uint16_t*>(a->w[2] ? a->w[2] : a->w[0]);
+  p.n0 = a->n[0];
+  p.n1 = a->epilogue == BZ_GEMV_SILU_MUL ? 0 : a->n[1];
+  p.ntot = ntot;
+  p.k = a->k;
+  p.kp = kp;
+  p.y = static_cast<uint16_t*>(a->y);
+  p.ldy = a->y_stride;
+  p.res = static_cast<const uint16_t*>(a->res);
+  p.ldr = a->res_stride;
+  const int rows_per_block = kGemvWaves * r;
+  const int grid = (ntot + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kGemvThreads), lds, stream, p);
+  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
+
+__attribute__((visibility("default"))) int bz_rmsnorm(const void* x, int64_t x_stride, const void* w, float eps,
+                                                       void* y, int64_t y_stride, int32_t m, int32_t k,
+                                                       hipStream_t stream) {
+  if (x == nullptr || w == nullptr || y == nullptr) return BZ_ERR_NULL;
+  if (m <= 0 || m > 65535 || k <= 0 || (k & 7) || x_stride < k || y_stride < k) return BZ_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || (x_stride & 7) || (y_stride & 7)) return BZ_ERR_ALIGNMENT;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(m), dim3(kGemvThreads), 0, stream, static_cast<const uint16_t*>(x), x_stride,
+                     static_cast<const uint16_t*>(w), eps, static_cast<uint16_t*>(y), y_stride, k);
+  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
+
+}  // extern "C"

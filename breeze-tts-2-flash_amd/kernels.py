@@ -22,20 +22,20 @@ REPO_DIR = PKG_DIR.parent
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libbz_gqa_decode.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["gqa_decode.hip", "gqa_fused.hip"]  # translation units, compiled in parallel
-HEADERS = ["gqa_kernels.cuh"]
+SOURCES = ["gqa_decode.hip", "gqa_fused.hip", "gemv.hip"]  # translation units, compiled in parallel
+HEADERS = ["gqa_kernels.cuh", "device_common.cuh"]
 ARCH = "gfx950"
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32)
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
     "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_fused", "bz_gqa_decode_workspace_size",
-    "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version",
+    "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version", "bz_gemv", "bz_rmsnorm",
 )
 
 MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
@@ -68,6 +68,21 @@ class GqaDecodeFusedArgs(ctypes.Structure):
         ("q_norm_weight", ctypes.c_void_p), ("k_norm_weight", ctypes.c_void_p), ("eps", ctypes.c_float),
         ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("rope_stride_b", ctypes.c_int64),
         ("cache_pos", ctypes.c_void_p),
+    ]
+
+
+GEMV_PLAIN, GEMV_RESIDUAL, GEMV_SILU_MUL = 0, 1, 2
+
+
+class GemvArgs(ctypes.Structure):
+    """Mirror of struct bz_gemv_args (include/bz_gemv.h)."""
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int64),
+        ("norm_weight", ctypes.c_void_p), ("eps", ctypes.c_float),
+        ("w", ctypes.c_void_p * 3), ("n", ctypes.c_int32 * 3),
+        ("res", ctypes.c_void_p), ("res_stride", ctypes.c_int64),
+        ("y", ctypes.c_void_p), ("y_stride", ctypes.c_int64),
+        ("m", ctypes.c_int32), ("k", ctypes.c_int32), ("epilogue", ctypes.c_int32),
     ]
 
 
@@ -133,6 +148,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_status_string.restype = ctypes.c_char_p
     lib.bz_gqa_decode_abi_version.argtypes = []
     lib.bz_gqa_decode_abi_version.restype = ctypes.c_int
+    lib.bz_gemv.argtypes = [P(GemvArgs), ctypes.c_void_p]
+    lib.bz_gemv.restype = ctypes.c_int
+    lib.bz_rmsnorm.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+                               ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+    lib.bz_rmsnorm.restype = ctypes.c_int
 
 
 def load() -> ctypes.CDLL:

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 3
+#define BZ_GQA_DECODE_ABI_VERSION 4
 
 typedef enum bz_status {
   BZ_OK = 0,

@@ -193,3 +193,66 @@ def test_fused_validation(lib, K, over, code):
     f = _good_fused(K, **over)
     assert lib.bz_gqa_decode_fused(ctypes.byref(f), None) == code
     assert lib.bz_gqa_decode_fused(None, None) == -1
+
+
+def test_gemv_struct_layout_matches_c(K, tmp_path):
+    fields = [f for f, _ in K.GemvArgs._fields_]
+    src = ["#include <stddef.h>", "#include <stdio.h>", '#include "bz_gemv.h"', "int main(void) {",
+           '  printf("size %zu\\n", sizeof(bz_gemv_args));']
+    src += [f'  printf("{f} %zu\\n", offsetof(bz_gemv_args, {f}));' for f in fields]
+    src += ["  return 0;", "}"]
+    c = tmp_path / "layout_gemv.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout_gemv"
+    subprocess.run(["gcc", "-std=c11", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{REPO / 'include'}",
+                    str(c), "-o", str(exe)], check=True)
+    got = dict(ln.split() for ln in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                   check=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(K.GemvArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(K.GemvArgs, f).offset, f
+
+
+def _good_gemv(K, **over):
+    """Backbone q|k|v projection sizes with fake (never dereferenced) addresses and no workspace-free launch: every
+    case below breaks one check, so nothing is launched."""
+    a = K.GemvArgs()
+    a.x, a.x_stride = 0x10000, 2048
+    a.w[0], a.w[1], a.w[2] = 0x100000, 0x200000, 0x300000
+    a.n[0], a.n[1], a.n[2] = 2048, 1024, 1024
+    a.y, a.y_stride = 0x40000, 4096
+    a.m, a.k, a.epilogue = 2, 2048, K.GEMV_PLAIN
+    for key, v in over.items():
+        if key.startswith("w") and key[1:].isdigit():
+            a.w[int(key[1:])] = v
+        elif key.startswith("n") and key[1:].isdigit():
+            a.n[int(key[1:])] = v
+        else:
+            setattr(a, key, v)
+    return a
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), -1), (dict(y=None), -1), (dict(w0=None), -1), (dict(w1=None), -1),
+    (dict(m=0), -2), (dict(m=5), -2), (dict(k=0), -2), (dict(k=2044), -2), (dict(n1=-1), -2),
+    (dict(n0=0, n1=0, n2=0), -2), (dict(x_stride=1024), -2), (dict(y_stride=4000), -2),
+    (dict(epilogue=3), -3), (dict(epilogue=1), -1), (dict(epilogue=1, res=0x50000, norm_weight=0x60000), -3),
+    (dict(epilogue=2, n1=2048, n2=0, w1=None), -1), (dict(epilogue=2, n1=1024, n2=0), -2),
+    (dict(epilogue=2, n1=2048, n2=1), -2),
+    (dict(x=0x10008), -4), (dict(x_stride=2052), -4), (dict(w2=0x300004), -4), (dict(norm_weight=0x60002), -4),
+    (dict(k=32768, x_stride=32768), -3),                      # x does not fit 64 KiB of LDS at m = 2
+])
+def test_gemv_validation(lib, K, over, code):
+    a = _good_gemv(K, **over)
+    assert lib.bz_gemv(ctypes.byref(a), None) == code
+    assert lib.bz_gemv(None, None) == -1
+
+
+def test_rmsnorm_validation(lib):
+    P = 0x10000
+    assert lib.bz_rmsnorm(None, 2048, P, 1e-6, P, 2048, 2, 2048, None) == -1
+    assert lib.bz_rmsnorm(P, 2048, P, 1e-6, P, 2048, 0, 2048, None) == -2
+    assert lib.bz_rmsnorm(P, 2048, P, 1e-6, P, 2048, 2, 2044, None) == -2
+    assert lib.bz_rmsnorm(P, 1024, P, 1e-6, P, 2048, 2, 2048, None) == -2
+    assert lib.bz_rmsnorm(P + 2, 2048, P, 1e-6, P, 2048, 2, 2048, None) == -4
+    assert lib.bz_rmsnorm(P, 2048, P, 1e-6, P, 2052, 2, 2048, None) == -4
