@@ -140,6 +140,102 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=F
     return us, read_bytes, nsets
 
 
+BACKBONE = dict(H=2048, nq=2048, nk=1024, inter=6144, layers=28, D=128, cap=2048, len=1024)
+
+
+def time_backbone(pkg, dev, steps):
+    """The reference's backbone decode step at its serving shape (a Qwen3 of hidden 2048, 16 q / 8 KV heads of 128,
+    intermediate 6144, 28 layers; the CFG pair, M = 2; KV 1024 of 2048 slots) on random-init weights: per layer
+    gemv_seg (RMSNorm + q|k|v) -> gqa_decode_fused -> gemv_resid (o_proj) -> gemv_gateup -> gemv_resid (down), then
+    the final rmsnorm (flash/backbone.py:120-129), one HIP graph per step. Also each GEMV alone, rotating over the 28
+    layers' weights. Returns {name: {us, bytes, GB/s}}."""
+    import torch
+
+    c = BACKBONE
+    H, nq, nk, I, L, D = c["H"], c["nq"], c["nk"], c["inter"], c["layers"], c["D"]
+    M = 2
+    gen = torch.Generator(device=dev).manual_seed(123)
+    bf = torch.bfloat16
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * scale).to(bf)
+
+    layers = []
+    for _ in range(L):
+        layers.append(dict(ln1=1 + rnd(H, scale=0.1), ln2=1 + rnd(H, scale=0.1), qn=1 + rnd(D, scale=0.1),
+                           kn=1 + rnd(D, scale=0.1), wq=rnd(nq, H, scale=H ** -0.5), wk=rnd(nk, H, scale=H ** -0.5),
+                           wv=rnd(nk, H, scale=H ** -0.5), wo=rnd(H, nq, scale=nq ** -0.5),
+                           wg=rnd(I, H, scale=H ** -0.5), wu=rnd(I, H, scale=H ** -0.5),
+                           wd=rnd(H, I, scale=I ** -0.5),
+                           kc=rnd(M, nk // D, c["cap"], D), vc=rnd(M, nk // D, c["cap"], D)))
+    norm_w = 1 + rnd(H, scale=0.1)
+    x0 = rnd(M, H)
+    qkv = torch.empty(M, nq + 2 * nk, dtype=bf, device=dev)
+    ao = torch.empty(M, nq // D, D, dtype=bf, device=dev)
+    h1 = torch.empty(M, H, dtype=bf, device=dev)
+    act = torch.empty(M, I, dtype=bf, device=dev)
+    xb = [torch.empty(M, H, dtype=bf, device=dev) for _ in range(2)]
+    hidden = torch.empty(M, H, dtype=bf, device=dev)
+    pos = c["len"] - 1
+    inv = 1e6 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = torch.cat([pos * inv] * 2)
+    cos = ang.cos().to(bf).expand(M, D).contiguous().to(dev)
+    sin = ang.sin().to(bf).expand(M, D).contiguous().to(dev)
+    cache_pos = torch.tensor([pos], dtype=torch.int64, device=dev)
+    lens = torch.full((M,), c["len"], dtype=torch.int32, device=dev)
+    eps, scale = 1e-6, D ** -0.5
+
+    def step():
+        x = x0
+        for i, ly in enumerate(layers):
+            pkg.gemv_seg(x, ly["ln1"], eps, ly["wq"], ly["wk"], ly["wv"], qkv)
+            pkg.gqa_decode_fused(qkv, ly["qn"], ly["kn"], eps, cos, sin, ly["kc"], ly["vc"], cache_pos, scale, ao,
+                                 seq_lens=lens)
+            pkg.gemv_resid(ao.view(M, nq), ly["wo"], x, h1)
+            pkg.gemv_gateup(h1, ly["ln2"], eps, ly["wg"], ly["wu"], act)
+            pkg.gemv_resid(act, ly["wd"], h1, xb[i % 2])
+            x = xb[i % 2]
+        pkg.rmsnorm(x, norm_w, eps, hidden)
+
+    def graph_time(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1000.0 / reps
+
+    out = {}
+    layer_bytes = 2 * ((nq + 2 * nk) * H + H * nq + 2 * I * H + H * I) + 2 * 2 * (nk // D) * c["len"] * D * M
+    us = graph_time(step, max(5, steps // 100))
+    out["backbone_step_28_layers"] = {"us": round(us, 1), "bytes": L * layer_bytes,
+                                      "GB/s": round(L * layer_bytes / us / 1e3, 1)}
+    # each GEMV alone, over the 28 layers' weights in turn (28 launches per replay)
+    cases = {
+        "gemv_qkv_norm": (lambda ly: pkg.gemv_seg(x0, ly["ln1"], eps, ly["wq"], ly["wk"], ly["wv"], qkv),
+                          2 * (nq + 2 * nk) * H),
+        "gemv_o_resid": (lambda ly: pkg.gemv_resid(ao.view(M, nq), ly["wo"], x0, h1), 2 * H * nq),
+        "gemv_gateup_norm_silu": (lambda ly: pkg.gemv_gateup(h1, ly["ln2"], eps, ly["wg"], ly["wu"], act),
+                                  2 * 2 * I * H),
+        "gemv_down_resid": (lambda ly: pkg.gemv_resid(act, ly["wd"], h1, hidden), 2 * H * I),
+    }
+    for name, (fn, wbytes) in cases.items():
+        us = graph_time(lambda: [fn(ly) for ly in layers], max(5, steps // 100)) / L
+        out[name] = {"us": round(us, 3), "weight_bytes": wbytes, "GB/s": round(wbytes / us / 1e3, 1),
+                     "pct_of_peak_hbm": round(100.0 * wbytes / us / 1e3 / PEAK_HBM_GBS, 1)}
+    del layers
+    return out
+
+
 def time_depth_frame(pkg, dev, steps, warmup):
     """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph."""
     import torch
@@ -322,6 +418,10 @@ def main():
         extra["config5_depth_frame"] = {"us_per_frame": round(us_f, 3), "us_per_call": round(us_f / 32, 3),
                                         "bytes_per_frame": fb, "GB/s": round(fb / us_f / 1e3, 1)}
         print(f"[bench] config 5 depth frame: {us_f:.3f} us/frame", file=sys.stderr, flush=True)
+        bb = time_backbone(pkg, dev, args.steps)
+        extra["backbone"] = bb
+        for k, v in bb.items():
+            print(f"[bench] {k}: {v}", file=sys.stderr, flush=True)
         line["extra"] = extra
     if not args.no_cpu:
         us_cpu, cores, n = cpu_baseline(w2, budget_s=30.0)

@@ -6,7 +6,8 @@
 //     streams them whole; lane l reads the 16 bytes at k = 8 l + 512 c of every chunk c, so one wave load instruction
 //     covers 1 KiB of one weight row. Rows are raw buffer resources cut at k (and empty past the last output row), so
 //     every load is unconditional, nothing past a row is read, and the compiler's vmcnt accounting stays exact.
-//   - two tiles of R x U chunks are in flight (ping-pong); the first two are issued before the x prologue.
+//   - two tiles of R x U chunks are in flight (ping-pong); the first two are issued before the x prologue, after x's
+//     own loads, so the prologue waits for x alone.
 //   - x (RMSNorm'ed at the eager rounding points when asked) is staged once per workgroup in LDS, zero-padded to a
 //     multiple of the tile, and read with one ds_read_b128 per chunk and row of x.
 //   - products: four v_dot2c_f32_bf16 per 16 bytes (bf16 x bf16 exact, fp32 accumulation); the R * M (2 R * M)
@@ -46,35 +47,62 @@ struct GemvParams {
   int64_t ldr;
 };
 
-// Stage x (m rows of k, zero-padded to kp) into LDS; with NORM, as bf16(w * bf16(x * rsqrt(mean(x^2) + eps))) with
-// the mean over the k real elements (bb_fused.cu:95-140).
+// x is staged in two steps. x_issue loads the first kXr 16-byte vectors per thread into registers before the weight
+// tiles are issued, so the prologue waits for x alone (loads complete in issue order). stage_x writes them to LDS,
+// loads any rest directly, and with NORM rewrites LDS as bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), the mean over
+// the k real elements (bb_fused.cu:95-140). One resource covers the x matrix; elements past k in a row (the row
+// padding, or past the last row) read as 0, so LDS holds x zero-padded to kp.
+constexpr int kXr = 4;
+
+template <int M>
+__device__ __forceinline__ uint4 x_vector(const GemvParams& p, const Rsrc& rx, int idx) {
+  const int kv = p.kp / 8;
+  const int m = idx / kv, j = idx - m * kv;
+  const bool in = idx < M * kv && j * 8 < p.k;
+  const uint32_t off = in ? (uint32_t)(m * p.ldx + j * 8) * 2 : 0xfffffff0u;  // out of range: reads 0
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+}
+
+template <int M>
+__device__ __forceinline__ void x_issue(const GemvParams& p, const Rsrc& rx, uint4 (&xr)[kXr]) {
+#pragma unroll
+  for (int i = 0; i < kXr; ++i) xr[i] = x_vector<M>(p, rx, threadIdx.x + i * kGemvThreads);
+}
+
 template <int M, bool NORM>
-__device__ __forceinline__ void stage_x(const GemvParams& p, uint16_t* xs) {
+__device__ __forceinline__ void stage_x(const GemvParams& p, const Rsrc& rx, const uint4 (&xr)[kXr], uint16_t* xs) {
   const int tid = threadIdx.x;
-  const int kv = p.kp / 8;  // 16-byte vectors per LDS row
+  const int kv = p.kp / 8, total = M * kv;
   float ss[M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    ss[m] = 0.f;
-    const Rsrc rx = span_rsrc(p.x + (int64_t)m * p.ldx, p.k * 2);
-    for (int j = tid; j < kv; j += kGemvThreads) {
-      const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, j * 16, 0, 0));
-      reinterpret_cast<uint4*>(xs + m * p.kp)[j] = v;
-      if (NORM) {
-        float f[8];
-        unpack8(v, f);
+  for (int m = 0; m < M; ++m) ss[m] = 0.f;
+  auto put = [&](int idx, const uint4& v) {
+    reinterpret_cast<uint4*>(xs)[idx] = v;  // LDS row pitch kp: vector idx of the [M][kp] array
+    if (NORM) {
+      float f[8];
+      unpack8(v, f);
+      float s2 = 0.f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) ss[m] = fmaf(f[t], f[t], ss[m]);
-      }
+      for (int t = 0; t < 8; ++t) s2 = fmaf(f[t], f[t], s2);
+      const int m = idx / kv;
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm)
+        if (mm == m) ss[mm] += s2;
     }
+  };
+#pragma unroll
+  for (int i = 0; i < kXr; ++i) {
+    const int idx = tid + i * kGemvThreads;
+    if (idx < total) put(idx, xr[i]);
   }
+  for (int idx = tid + kXr * kGemvThreads; idx < total; idx += kGemvThreads) put(idx, x_vector<M>(p, rx, idx));
   if (!NORM) return;
   __shared__ float red[kGemvWaves][M];
   const int lane = tid % kWave, wave = tid / kWave;
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const float s = wave_sum(ss[m]);
-    if (lane == 0) red[wave][m] = s;
+    const float s2 = wave_sum(ss[m]);
+    if (lane == 0) red[wave][m] = s2;
   }
   __syncthreads();
   const Rsrc rw = span_rsrc(p.nw, p.k * 2);
@@ -99,7 +127,16 @@ __device__ __forceinline__ void stage_x(const GemvParams& p, uint16_t* xs) {
   }
 }
 
-template <int M, int R, bool NORM, int EPI>
+// x of one lane in registers: row m, chunk c (k = 512 c + 8 lane), zero past k.
+__device__ __forceinline__ uint4 x_chunk(const GemvParams& p, const Rsrc& rx, int m, int c, int lane) {
+  const int k0 = c * kChunk + lane * 8;
+  const uint32_t off = k0 < p.k ? (uint32_t)(m * p.ldx + k0) * 2 : 0xfffffff0u;
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+}
+
+// KC > 0: x held in registers, KC chunks per lane (k <= 512 KC <= 2 tiles): no LDS, and the RMSNorm's sum of squares
+// is reduced over the wave, so the prologue needs no barrier. KC == 0: x staged in LDS (any k).
+template <int M, int R, bool NORM, int EPI, int KC>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) {
   constexpr int NR = EPI == BZ_GEMV_SILU_MUL ? 2 * R : R;  // weight rows per wave
   extern __shared__ __align__(16) uint16_t xs[];            // [M][kp] bf16
@@ -134,44 +171,100 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) 
         t[r][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr[r], off, 0, kStream));
     }
   };
-  // the first two weight tiles do not depend on x: issue them before the prologue
-  load(ta, 0);
-  load(tb, 1);
-  __builtin_amdgcn_sched_barrier(0);
-
-  stage_x<M, NORM>(p, xs);
-  __syncthreads();
-
+  const Rsrc rx = span_rsrc(p.x, (int)(((int64_t)(M - 1) * p.ldx + p.k) * 2));
   float acc[NR][M];
 #pragma unroll
   for (int r = 0; r < NR; ++r)
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
-  auto consume = [&](const uint4 (&t)[NR][kU], int it) {
+  auto dot16 = [](const uint4& w, const uint4& xv, float a) {
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
+  };
+
+  if constexpr (KC > 0) {
+    static_assert(KC <= 2 * kU, "x in registers: the row fits the first two tiles");
+    // x (and the norm weight) first, then both weight tiles; the prologue waits for x alone
+    uint4 xv[M][KC], nwv[KC];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int kk = it * kTileK + u * kChunk + lane * 8;
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int c = 0; c < KC; ++c) xv[m][c] = x_chunk(p, rx, m, c, lane);
+    if (NORM) {
+      const Rsrc rw = span_rsrc(p.nw, p.k * 2);
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+        nwv[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (c * kChunk + lane * 8) * 2, 0, 0));
+    }
+    load(ta, 0);
+    load(tb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (NORM) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xs + m * p.kp + kk);
+        float ss = 0.f;
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          float a = acc[r][m];
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t[r][u].w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
-          acc[r][m] = a;
+        for (int c = 0; c < KC; ++c) {
+          float f[8];
+          unpack8(xv[m][c], f);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) ss = fmaf(f[t], f[t], ss);
+        }
+        const float rs = rsqrtf(wave_sum(ss) * (1.f / (float)p.k) + p.eps);
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          float f[8], w[8];
+          unpack8(xv[m][c], f);
+          unpack8(nwv[c], w);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) f[t] *= rs;
+          round8(f);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) f[t] *= w[t];
+          xv[m][c] = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                                pack_bf16x2(f[6], f[7]));
         }
       }
     }
-  };
-  const int nit = p.kp / kTileK;
-  for (int it = 0; it < nit; it += 2) {
-    consume(ta, it);
-    load(ta, it + 2);  // past k: reads 0 without a memory access
-    if (it + 1 < nit) consume(tb, it + 1);
-    load(tb, it + 3);
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          acc[r][m] = dot16(c < kU ? ta[r][c % kU] : tb[r][c % kU], xv[m][c], acc[r][m]);
+  } else {
+    // x first (the prologue then waits for x alone), then the first two weight tiles, all before the prologue
+    uint4 xr[kXr];
+    x_issue<M>(p, rx, xr);
+    load(ta, 0);
+    load(tb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    stage_x<M, NORM>(p, rx, xr, xs);
+    __syncthreads();
+
+    auto consume = [&](const uint4 (&t)[NR][kU], int it) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int kk = it * kTileK + u * kChunk + lane * 8;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xs + m * p.kp + kk);
+#pragma unroll
+          for (int r = 0; r < NR; ++r) acc[r][m] = dot16(t[r][u], xv, acc[r][m]);
+        }
+      }
+    };
+    const int nit = p.kp / kTileK;
+    for (int it = 0; it < nit; it += 2) {
+      consume(ta, it);
+      load(ta, it + 2);  // past k: reads 0 without a memory access
+      if (it + 1 < nit) consume(tb, it + 1);
+      load(tb, it + 3);
+    }
   }
 
   // sum the accumulators over the wave: DPP inside each 16-lane row, then transposed swaps across the 4 rows, so
@@ -253,39 +346,59 @@ __global__ void __launch_bounds__(kGemvThreads) rmsnorm_kernel(const uint16_t* x
 
 using GemvFn = void (*)(const GemvParams);
 
-template <int M, int R>
+template <int M, int R, int KC>
 GemvFn pick_epi(int epi, bool norm) {
-  if (epi == BZ_GEMV_PLAIN) return norm ? gemv_kernel<M, R, true, BZ_GEMV_PLAIN> : gemv_kernel<M, R, false, BZ_GEMV_PLAIN>;
-  if (epi == BZ_GEMV_RESIDUAL) return norm ? nullptr : gemv_kernel<M, R, false, BZ_GEMV_RESIDUAL>;
+  if (epi == BZ_GEMV_PLAIN)
+    return norm ? gemv_kernel<M, R, true, BZ_GEMV_PLAIN, KC> : gemv_kernel<M, R, false, BZ_GEMV_PLAIN, KC>;
+  if (epi == BZ_GEMV_RESIDUAL) return norm ? nullptr : gemv_kernel<M, R, false, BZ_GEMV_RESIDUAL, KC>;
   if (epi == BZ_GEMV_SILU_MUL)
-    return norm ? gemv_kernel<M, R, true, BZ_GEMV_SILU_MUL> : gemv_kernel<M, R, false, BZ_GEMV_SILU_MUL>;
+    return norm ? gemv_kernel<M, R, true, BZ_GEMV_SILU_MUL, KC> : gemv_kernel<M, R, false, BZ_GEMV_SILU_MUL, KC>;
   return nullptr;
 }
 
-template <int M>
+template <int M, int KC>
 GemvFn pick_r(int r, int epi, bool norm) {
   switch (r) {
-    case 1: return pick_epi<M, 1>(epi, norm);
-    case 2: return pick_epi<M, 2>(epi, norm);
-    default: return pick_epi<M, 4>(epi, norm);
+    case 1: return pick_epi<M, 1, KC>(epi, norm);
+    case 2: return pick_epi<M, 2, KC>(epi, norm);
+    default: return pick_epi<M, 4, KC>(epi, norm);
   }
 }
 
-GemvFn pick_gemv(int m, int r, int epi, bool norm) {
+// x in registers for m * chunks <= 8 with m <= 2 (KC = 4: k <= 2048) or m <= 4 (KC = 2: k <= 1024); LDS otherwise.
+template <int M>
+GemvFn pick_kc(int kc, int r, int epi, bool norm) {
+  if constexpr (M <= 2) {
+    if (kc == 4) return pick_r<M, 4>(r, epi, norm);
+  }
+  if (kc == 2) return pick_r<M, 2>(r, epi, norm);
+  return pick_r<M, 0>(r, epi, norm);
+}
+
+// Chunks of x per lane held in registers (0: x in LDS).
+int kc_for(int m, int k) {
+  const int chunks = (k + kChunk - 1) / kChunk;
+  return chunks <= 2 ? 2 : (chunks <= 4 && m <= 2 ? 4 : 0);
+}
+
+GemvFn pick_gemv(int m, int kc, int r, int epi, bool norm) {
   switch (m) {
-    case 1: return pick_r<1>(r, epi, norm);
-    case 2: return pick_r<2>(r, epi, norm);
-    case 3: return pick_r<3>(r, epi, norm);
-    case 4: return pick_r<4>(r, epi, norm);
+    case 1: return pick_kc<1>(kc, r, epi, norm);
+    case 2: return pick_kc<2>(kc, r, epi, norm);
+    case 3: return pick_kc<3>(kc, r, epi, norm);
+    case 4: return pick_kc<4>(kc, r, epi, norm);
     default: return nullptr;
   }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Output rows per wave: enough waves to keep every CU's SIMDs streaming (about 8 waves per CU or more).
-int rows_per_wave(int ntot, int epi) {
+// Output rows per wave. With x in registers every wave loads its own x, so two rows per wave halve that L2 traffic
+// (measured at the backbone shapes: q|k|v 6.6 -> 5.3 us, o_proj 3.7 -> 3.55 us); with x in LDS, one row per wave
+// keeps more waves streaming until the rows are many (down: 7.2 us with two rows, 6.9 with one).
+int rows_per_wave(int ntot, int epi, int kc) {
   const int rows = epi == BZ_GEMV_SILU_MUL ? 2 * ntot : ntot;
+  if (kc > 0) return 2;
   if (rows >= 16384) return 4;
   if (rows >= 8192) return 2;
   return 1;
@@ -324,9 +437,11 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   const int kp = (a->k + kTileK - 1) / kTileK * kTileK;
   const size_t lds = (size_t)a->m * kp * 2;
   if (lds > (size_t)kMaxLds || (int64_t)a->k * 2 > INT32_MAX) return BZ_ERR_UNSUPPORTED;
+  if (((int64_t)(a->m - 1) * a->x_stride + a->k) * 2 > INT32_MAX) return BZ_ERR_SHAPE;  // x: 32-bit byte offsets
 
-  const int r = rows_per_wave(ntot, a->epilogue);
-  GemvFn fn = pick_gemv(a->m, r, a->epilogue, a->norm_weight != nullptr);
+  const int kc = kc_for(a->m, a->k);
+  const int r = rows_per_wave(ntot, a->epilogue, kc);
+  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr);
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   GemvParams p;
   p.x = static_cast<const uint16_t*>(a->x);
@@ -347,7 +462,7 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   p.ldr = a->res_stride;
   const int rows_per_block = kGemvWaves * r;
   const int grid = (ntot + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(kGemvThreads), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kGemvThreads), kc > 0 ? 0 : lds, stream, p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
