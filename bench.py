@@ -41,6 +41,8 @@ def parse_args():
     p.add_argument("--fused", action="store_true",
                    help="time the fused decode step (bz_gqa_decode_fused) instead of attention alone")
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
+    p.add_argument("--backbone-only", action="store_true",
+                   help="only the 28-layer backbone decode step and its GEMVs (for profiling)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--traffic-bytes", type=float, default=None,
                    help="HBM bytes per call (overrides the value read from profiles/)")
@@ -364,6 +366,10 @@ def main():
         return
     pkg.load()
 
+    if args.backbone_only:
+        bb = time_backbone(pkg, dev, args.steps)
+        print(json.dumps({"backbone": bb}), flush=True)
+        return
     cfg = args.config
     w2 = workloads.make(cfg)
     splits2 = args.splits or pkg.default_splits(w2.batch, w2.num_kv_heads, w2.head_dim, w2.capacity, 0)
