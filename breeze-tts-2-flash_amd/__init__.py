@@ -7,15 +7,17 @@ Public API:
   attn_decode(query, kc, vc, mask, scaling, scores, cmax, part, counters, out, dbg=None)   (reference order)
   attn_decode_fused(qkv, qn_w, kn_w, eps, cos, sin, kc, vc, mask, cache_pos, scaling, ..., out, dbg=None)
   gemv_seg / gemv_resid / gemv_gateup / rmsnorm   backbone decode GEMVs (reference order; C ABI include/bz_gemv.h)
+  mask_interval(mask, capacity, ...)   the [kv_start, seq_lens) rows of an interval mask, once per decode step
+  backbone.fused_decode_step(graph) / backbone.install(BackboneGraph)   the whole backbone decode step
   build() / load()   compile / open libbz_gqa_decode.so (C ABI: include/bz_gqa_decode.h, include/bz_gemv.h)
 """
 from .attention import (default_splits, get_workspace, gqa_decode, gqa_decode_fused, gqa_decode_masked,
-                        workspace_bytes)
+                        mask_interval, workspace_bytes)
 from .compat import attn_decode, attn_decode_fused
 from .gemv import gemv_gateup, gemv_resid, gemv_seg, rmsnorm
 from .kernels import build, load
-from . import hf_attention
+from . import backbone, hf_attention
 
 __all__ = ["gqa_decode", "gqa_decode_masked", "gqa_decode_fused", "attn_decode", "attn_decode_fused",
-           "gemv_seg", "gemv_resid", "gemv_gateup", "rmsnorm",
+           "gemv_seg", "gemv_resid", "gemv_gateup", "rmsnorm", "mask_interval", "backbone",
            "workspace_bytes", "default_splits", "get_workspace", "build", "load"]

@@ -194,6 +194,31 @@ def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     return out
 
 
+def mask_interval(mask: torch.Tensor, capacity: int, batch: int | None = None,
+                  seq_lens: torch.Tensor | None = None,
+                  kv_start: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(seq_lens, kv_start): per row, the interval [kv_start, seq_lens) of positions < capacity whose mask value is
+    > -1e30 (bz_mask_interval), the range gqa_decode_masked derives on the device, computed once for the layers of
+    a decode step that share the mask. mask: [B or 1, 1, 1, >= capacity] bf16 / fp32 (or [B or 1, >= capacity]);
+    batch defaults to the mask's; seq_lens / kv_start: optional int32 [B] device outputs. Returns them."""
+    _check(mask.is_cuda, "mask must be a device tensor")
+    B = mask.size(0) if batch is None else int(batch)
+    code, stride_b = _mask_view(mask, B, capacity)
+    dev = mask.device
+    if seq_lens is None:
+        seq_lens = torch.empty(B, dtype=torch.int32, device=dev)
+    if kv_start is None:
+        kv_start = torch.empty(B, dtype=torch.int32, device=dev)
+    _int32_rows(seq_lens, B, "seq_lens", dev)
+    _int32_rows(kv_start, B, "kv_start", dev)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        kernels.check(kernels.load().bz_mask_interval(mask.data_ptr(), code, stride_b, B, int(capacity),
+                                                      seq_lens.data_ptr(), kv_start.data_ptr(),
+                                                      ctypes.c_void_p(stream)), "bz_mask_interval")
+    return seq_lens, kv_start
+
+
 def gqa_decode_fused(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
                      cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      cache_pos: torch.Tensor, scale: float, out: torch.Tensor | None = None, *,

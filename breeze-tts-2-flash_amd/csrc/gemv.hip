@@ -8,8 +8,10 @@
 //     every load is unconditional, nothing past a row is read, and the compiler's vmcnt accounting stays exact.
 //   - two tiles of R x U chunks are in flight (ping-pong); the first two are issued before the x prologue, after x's
 //     own loads, so the prologue waits for x alone.
-//   - x (RMSNorm'ed at the eager rounding points when asked) is staged once per workgroup in LDS, zero-padded to a
-//     multiple of the tile, and read with one ds_read_b128 per chunk and row of x.
+//   - x (RMSNorm'ed at the eager rounding points when asked) is held in registers when it fits (k <= 1024, or
+//     k <= 2048 with M <= 2: every lane keeps its own 16 bytes of each chunk, and the norm's sum of squares is reduced
+//     over the wave, so there is no LDS and no barrier); otherwise it is staged once per workgroup in LDS,
+//     zero-padded to a multiple of the tile, and read with one ds_read_b128 per chunk and row of x.
 //   - products: four v_dot2c_f32_bf16 per 16 bytes (bf16 x bf16 exact, fp32 accumulation); the R * M (2 R * M)
 //     accumulators are summed over the wave with DPP inside 16-lane rows and transposed permlane swaps across rows,
 //     so each lane of a row ends with one finished output, written with the epilogue by that row's first lane.

@@ -322,6 +322,26 @@ __attribute__((visibility("default"))) int bz_gqa_decode_fused(const bz_gqa_deco
   return launch(a, stream, end, start, a->mask_dtype, f);
 }
 
+__attribute__((visibility("default"))) int bz_mask_interval(const void* mask, int32_t mask_dtype,
+                                                            int64_t mask_stride_b, int32_t batch, int32_t capacity,
+                                                            int32_t* seq_lens, int32_t* kv_start, hipStream_t stream) {
+  if (mask == nullptr || seq_lens == nullptr || kv_start == nullptr) return BZ_ERR_NULL;
+  if (mask_dtype != BZ_MASK_BF16 && mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  if (batch <= 0 || capacity <= 0 || mask_stride_b < 0 || (batch > 1 && mask_stride_b > 0 && mask_stride_b < capacity))
+    return BZ_ERR_SHAPE;
+  const size_t esize = mask_dtype == BZ_MASK_BF16 ? 2 : 4;
+  if ((reinterpret_cast<uintptr_t>(mask) % esize) || (reinterpret_cast<uintptr_t>(seq_lens) & 3) ||
+      (reinterpret_cast<uintptr_t>(kv_start) & 3))
+    return BZ_ERR_ALIGNMENT;
+  if (mask_dtype == BZ_MASK_BF16)
+    hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_BF16>, dim3(batch), dim3(kThreads), 0, stream, mask, mask_stride_b,
+                       capacity, kv_start, seq_lens);
+  else
+    hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_F32>, dim3(batch), dim3(kThreads), 0, stream, mask, mask_stride_b,
+                       capacity, kv_start, seq_lens);
+  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
+
 __attribute__((visibility("default"))) int bz_gqa_decode_workspace_size(int32_t batch, int32_t num_q_heads,
                                                                         int32_t num_kv_heads, int32_t head_dim,
                                                                         int32_t capacity, int32_t num_splits,

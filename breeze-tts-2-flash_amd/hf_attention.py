@@ -11,8 +11,11 @@ Routing:
   - q_len == 1, bf16 CUDA tensors, head_dim 64 / 128, group size 1 / 2 / 4 / 8, no dropout: bz_gqa_decode_masked (the
     range of each row comes from the mask on the device, left padding included) or, with no mask, bz_gqa_decode over
     the whole key length. A missing or broken library raises; there is no silent fallback for these calls.
-  - anything else (prefill, other dtypes or shapes, CPU tensors): the model's own eager attention, exactly as
-    without this module. calls["hip"] / calls["eager"] count the two routes.
+  - anything else (prefill, other dtypes or shapes, CPU tensors): eager attention. CPU tensors get the model's own
+    eager function, exactly as without this module; GPU tensors get eager_attention below, the same rounding points
+    with every operand of the batched products made contiguous (a bf16 batched product whose right operand is a
+    transposed view, as in the eager function's q @ k^T, is kept off the GPU). calls["hip"] / calls["eager"] count
+    the two routes.
 
 The mask: transformers builds no mask for attention implementations it does not know, so install() also registers
 transformers' eager mask builder under the same name; the function then gets the eager [B, 1, q_len, kv_len] mask
@@ -28,15 +31,39 @@ import torch
 from .attention import gqa_decode, gqa_decode_masked
 
 NAME = "mi355_decode"
+EAGER_NAME = "mi355_eager"   # eager_attention alone, for reference runs of a model on the GPU
 calls = {"hip": 0, "eager": 0}
 
 _SUPPORTED_D = (64, 128)
 _SUPPORTED_G = (1, 2, 4, 8)
 
 
-def _eager(module):
-    """The eager attention of the module's own model file (Qwen3: modeling_qwen3.eager_attention_forward), else
-    transformers' SDPA forward, which takes the same additive mask."""
+def eager_attention(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                    attention_mask: torch.Tensor | None, scaling: float | None = None, dropout: float = 0.0,
+                    **kwargs):
+    """Eager attention at the rounding points of transformers' eager_attention_forward (modeling_qwen3): KV heads
+    repeated for their group (q head h reads KV head h // G), scores = (q @ k^T in the input dtype) * scaling, plus the
+    additive mask, softmax in fp32 rounded back to the input dtype, then @ v. Both products take contiguous operands.
+    Returns (attn_output [B, q_len, NH, D], weights)."""
+    G = query.size(1) // key.size(1)
+    k = key.repeat_interleave(G, dim=1) if G > 1 else key
+    v = value.repeat_interleave(G, dim=1) if G > 1 else value
+    if scaling is None:
+        scaling = query.size(-1) ** -0.5
+    w = torch.matmul(query.contiguous(), k.transpose(2, 3).contiguous()) * scaling
+    if attention_mask is not None:
+        w = w + attention_mask[:, :, :, :k.size(2)]
+    w = torch.softmax(w, dim=-1, dtype=torch.float32).to(query.dtype)
+    w = torch.nn.functional.dropout(w, p=dropout, training=module.training)
+    out = torch.matmul(w, v.contiguous())
+    return out.transpose(1, 2).contiguous(), w
+
+
+def _eager(module, query):
+    """GPU tensors: eager_attention. CPU tensors: the eager attention of the module's own model file (Qwen3:
+    modeling_qwen3.eager_attention_forward), else transformers' SDPA forward, which takes the same additive mask."""
+    if query.is_cuda:
+        return eager_attention
     fn = getattr(sys.modules.get(type(module).__module__), "eager_attention_forward", None)
     if fn is None:
         from transformers.integrations.sdpa_attention import sdpa_attention_forward as fn
@@ -72,7 +99,8 @@ def mi355_decode_attention(module, query: torch.Tensor, key: torch.Tensor, value
     """Attention with the eager signature; q_len == 1 runs the gfx950 split-K kernel (see the module docstring)."""
     if not _hip_route(module, query, key, value, attention_mask, dropout):
         calls["eager"] += 1
-        return _eager(module)(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
+        return _eager(module, query)(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout,
+                                     **kwargs)
     calls["hip"] += 1
     B, NH, _, D = query.shape
     if scaling is None:
@@ -87,12 +115,14 @@ def mi355_decode_attention(module, query: torch.Tensor, key: torch.Tensor, value
 
 
 def install() -> str:
-    """Register the attention function and the eager mask builder under NAME (idempotent). Returns NAME: pass it as
-    attn_implementation (from_pretrained / from_config) or set it on a config, as the reference does with its own
-    implementation (flash/prefill_attn.py:41-46)."""
+    """Register the attention function and the eager mask builder under NAME, and eager_attention under EAGER_NAME
+    (idempotent). Returns NAME: pass it as attn_implementation (from_pretrained / from_config) or set it on a config,
+    as the reference does with its own implementation (flash/prefill_attn.py:41-46)."""
     from transformers import AttentionInterface
     from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, eager_mask
 
     AttentionInterface.register(NAME, mi355_decode_attention)
     ALL_MASK_ATTENTION_FUNCTIONS.register(NAME, eager_mask)
+    AttentionInterface.register(EAGER_NAME, eager_attention)
+    ALL_MASK_ATTENTION_FUNCTIONS.register(EAGER_NAME, eager_mask)
     return NAME

@@ -30,12 +30,13 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
     "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_fused", "bz_gqa_decode_workspace_size",
     "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version", "bz_gemv", "bz_rmsnorm",
+    "bz_mask_interval",
 )
 
 MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
@@ -153,6 +154,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_rmsnorm.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
                                ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.bz_rmsnorm.restype = ctypes.c_int
+    lib.bz_mask_interval.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.bz_mask_interval.restype = ctypes.c_int
 
 
 def load() -> ctypes.CDLL:

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 4
+#define BZ_GQA_DECODE_ABI_VERSION 5
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -150,6 +150,16 @@ typedef struct bz_gqa_decode_fused_args {
    Replaces attn_decode_fused (flash/csrc/bb_attn.cu:433-460, prologue :78-149, pybind :466-469), the entry the
    reference's decode step calls (flash/backbone.py:123-124). */
 int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* args, hipStream_t stream);
+
+/* Per row b, the interval [kv_start[b], seq_lens[b]) of positions p < capacity whose additive mask value is > -1e30
+   ([0, 0) for a row with none): the range bz_gqa_decode_masked and the mask form of bz_gqa_decode_fused derive on the
+   device, written to caller buffers so that one launch serves every layer of a decode step, whose layers share one
+   mask, and the per-layer calls pass seq_lens / kv_start. Inverts the reference's mask construction from pad_lens
+   and the position (third_party/breeze-tts/models/cudagraph/backbone_graph.py:239-252), which its attention
+   re-reads per layer to skip masked chunks (flash/csrc/bb_attn.cu:102-140). mask: bz_mask_dtype BF16 or F32, row b
+   at mask + b*mask_stride_b (0 broadcasts one row); seq_lens, kv_start: int32 [batch] device arrays. */
+int bz_mask_interval(const void* mask, int32_t mask_dtype, int64_t mask_stride_b, int32_t batch, int32_t capacity,
+                     int32_t* seq_lens, int32_t* kv_start, hipStream_t stream);
 
 /* Human-readable text of a bz_status. */
 const char* bz_status_string(int status);

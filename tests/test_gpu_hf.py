@@ -2,7 +2,8 @@
 (the reference backbone's layer type: q_norm / k_norm, RoPE, GQA 16 q / 8 KV heads, head_dim 128), bf16 on the GPU,
 left-padded batch of 2, greedy generation with a StaticCache and with a DynamicCache. Every q_len == 1 call must take
 the HIP route and match the fp32 oracle on the exact tensors the model passed (|d| <= 2e-3 + 1e-2 |ref|); the
-end-to-end logits must stay close to the same model run with attn_implementation="eager"."""
+end-to-end logits must stay close to the same model run with eager attention (hf_attention.EAGER_NAME: transformers'
+eager rounding points with contiguous operands, so no bf16 batched product takes a transposed view on the GPU)."""
 import numpy as np
 import pytest
 import torch
@@ -60,7 +61,7 @@ def test_qwen3_decode_through_registered_attention(device, cache):
     am[1, :9] = 0  # left padding: row 1 attends from position 9
     hip0 = hf_attention.calls["hip"]
     ours = generate(tiny_qwen3(REC, device), ids, am, cache)
-    ref = generate(tiny_qwen3("eager", device), ids, am, cache)
+    ref = generate(tiny_qwen3(hf_attention.EAGER_NAME, device), ids, am, cache)
 
     # 4 decode forwards (the first new token comes from prefill) x 2 layers, all on the HIP route
     assert hf_attention.calls["hip"] - hip0 == 8 and len(records) == 8
@@ -73,7 +74,7 @@ def test_qwen3_decode_through_registered_attention(device, cache):
         excess = np.abs(got - oracle) - (2e-3 + 1e-2 * np.abs(oracle))
         assert excess.max() <= 0, f"call {i}: excess {excess.max():.3e}"
 
-    # end to end against transformers' eager bf16 attention: the prefill logits are the same computation; decode
+    # end to end against eager bf16 attention: the prefill logits are the same computation; decode
     # logits differ only by the attention's rounding (eager rounds scores and probabilities to bf16)
     assert torch.equal(ours.logits[0], ref.logits[0])
     steps = 1

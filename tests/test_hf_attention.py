@@ -29,6 +29,7 @@ def test_install_registers_attention_and_mask():
     assert name == hf_attention.NAME
     assert AttentionInterface._global_mapping[name] is hf_attention.mi355_decode_attention
     assert ALL_MASK_ATTENTION_FUNCTIONS._global_mapping[name] is eager_mask
+    assert AttentionInterface._global_mapping[hf_attention.EAGER_NAME] is hf_attention.eager_attention
     assert hf_attention.install() == name  # idempotent
 
 
@@ -48,3 +49,23 @@ def test_cpu_model_routes_to_eager_bit_identically():
         assert torch.equal(a, b)
     assert hf_attention.calls["hip"] == before["hip"]
     assert hf_attention.calls["eager"] == before["eager"] + 3 * 2  # prefill + 2 decode steps, 2 layers
+
+
+@pytest.mark.parametrize("q_len,G", [(1, 2), (7, 2), (7, 1), (5, 4)])
+def test_eager_attention_matches_transformers_eager(q_len, G):
+    """eager_attention (the GPU route for prefill and other non-decode calls) gives transformers' eager attention bit
+    for bit: same rounding points, only the operands' memory layout differs."""
+    g = torch.Generator().manual_seed(q_len * 10 + G)
+    B, NKV, L, D = 2, 2, 19, 64
+    q = torch.randn(B, NKV * G, q_len, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, NKV, L, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, NKV, L, D, generator=g).to(torch.bfloat16)
+    mask = torch.zeros(B, 1, q_len, L, dtype=torch.bfloat16)
+    mask[1, :, :, :4] = torch.finfo(torch.bfloat16).min
+    mask[0, :, :, 10:12] = -1.5
+    mod = torch.nn.Module()
+    mod.num_key_value_groups = G
+    mod.eval()
+    want, want_w = qwen3.eager_attention_forward(mod, q, k, v, mask, scaling=D ** -0.5)
+    got, got_w = hf_attention.eager_attention(mod, q, k, v, mask, scaling=D ** -0.5)
+    assert torch.equal(got, want) and torch.equal(got_w, want_w)

@@ -8,7 +8,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
-from oracle.gemv import gemv, rmsnorm
+from oracle.gemv import decoder_layer, gemv, rmsnorm
 
 qwen3 = pytest.importorskip("transformers.models.qwen3.modeling_qwen3")
 
@@ -114,3 +114,73 @@ def test_planted_mistakes_caught():
     xf = bf16_to_f32(xs)
     bad = f32_to_bf16(bf16_to_f32(f32_to_bf16(xf / (np.sqrt((xf ** 2).mean(-1, keepdims=True)) + 0.5))))
     assert not within_ulp(bad, rmsnorm(xs, nw, 0.5), 0.5)
+
+
+def _fp32_attention(module, query, key, value, attention_mask, scaling, dropout=0.0, **kwargs):
+    """fp32 softmax attention over the whole cache (one query token, no mask), KV heads expanded by h // G, output
+    rounded to bf16: the attention the oracle restates (float64 there)."""
+    G = query.shape[1] // key.shape[1]
+    k = key.float().repeat_interleave(G, dim=1)
+    v = value.float().repeat_interleave(G, dim=1)
+    p = torch.softmax(query.float() @ k.transpose(-1, -2) * scaling, dim=-1)
+    return (p @ v).to(query.dtype).transpose(1, 2).contiguous(), None
+
+
+def test_decoder_layer_matches_transformers():
+    """oracle.gemv.decoder_layer (the reference's per-layer chain, flash/backbone.py:122-128) against transformers'
+    Qwen3DecoderLayer in bf16 on the CPU, one decode token per row over a DynamicCache holding 37 earlier positions,
+    with the attention computed in fp32 on both sides: the output, the new cache slot's k (normed, roped) and v."""
+    from transformers import AttentionInterface, DynamicCache, Qwen3Config
+
+    AttentionInterface.register("oracle_pin_fp32", _fp32_attention)
+    H, NH, NKV, D, INTER, B, L = 256, 4, 2, 64, 512, 2, 37
+    cfg = Qwen3Config(vocab_size=16, hidden_size=H, intermediate_size=INTER, num_hidden_layers=1,
+                      num_attention_heads=NH, num_key_value_heads=NKV, head_dim=D, rms_norm_eps=1e-6,
+                      max_position_embeddings=128)
+    cfg._attn_implementation = "oracle_pin_fp32"
+    torch.manual_seed(5)
+    layer = qwen3.Qwen3DecoderLayer(cfg, layer_idx=0).eval()
+    with torch.no_grad():
+        for name, prm in layer.named_parameters():
+            if "norm" in name:
+                prm.copy_(1 + 0.1 * torch.randn_like(prm))
+            else:
+                prm.copy_(torch.randn_like(prm) * prm.shape[1] ** -0.5)
+    layer = layer.to(torch.bfloat16)
+    rot = qwen3.Qwen3RotaryEmbedding(cfg)
+    rng = np.random.default_rng(6)
+    k_prev, v_prev = _bf16(rng, B, NKV, L, D), _bf16(rng, B, NKV, L, D)
+    x = _bf16(rng, B, H, scale=2.0)
+    xt = _t(x)[:, None]
+    pos_ids = torch.full((B, 1), L, dtype=torch.long)
+    cos, sin = rot(xt, pos_ids)
+    cache = DynamicCache()
+    cache.update(_t(k_prev), _t(v_prev), 0)
+    with torch.no_grad():
+        ref = layer(xt, attention_mask=None, position_ids=pos_ids, past_key_values=cache, use_cache=True,
+                    position_embeddings=(cos, sin))
+    ref = _bits(ref[:, 0])
+    k_ref, v_ref = (_bits(t[:, :, L]) for t in (cache.layers[0].keys, cache.layers[0].values))
+
+    sd = {n: _bits(t) for n, t in layer.state_dict().items()}
+    p = dict(ln1=sd["input_layernorm.weight"], ln2=sd["post_attention_layernorm.weight"],
+             qn=sd["self_attn.q_norm.weight"], kn=sd["self_attn.k_norm.weight"], wq=sd["self_attn.q_proj.weight"],
+             wk=sd["self_attn.k_proj.weight"], wv=sd["self_attn.v_proj.weight"], wo=sd["self_attn.o_proj.weight"],
+             wg=sd["mlp.gate_proj.weight"], wu=sd["mlp.up_proj.weight"], wd=sd["mlp.down_proj.weight"], eps=1e-6,
+             qk_eps=1e-6, scale=D ** -0.5)
+    kc = np.zeros((B, NKV, L + 1, D), np.uint16)
+    vc = np.zeros_like(kc)
+    kc[:, :, :L], vc[:, :, :L] = k_prev, v_prev
+    r = bf16_to_f32(ref).astype(np.float64)
+    rms = np.sqrt((r ** 2).mean())
+
+    def close(params):
+        out, k2, v2 = decoder_layer(x, params, _bits(cos[:, 0]), _bits(sin[:, 0]), kc, vc, L, np.full(B, L + 1))
+        g = bf16_to_f32(out).astype(np.float64)
+        return bool(np.array_equal(v2[:, :, L], v_ref) and within_ulp(k2[:, :, L], k_ref, 0.98)
+                    and (np.abs(g - r) <= 2.0 ** -6 * np.abs(r) + 2.0 ** -6 * rms).all() and (out == ref).mean() >= 0.9)
+
+    assert close(p)
+    # planted mistakes: the two layer norms' weights swapped; the MLP's gate and up swapped
+    assert not close({**p, "ln1": p["ln2"], "ln2": p["ln1"]})
+    assert not close({**p, "wg": p["wu"], "wu": p["wg"]})
