@@ -156,7 +156,7 @@ int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* args, hipStream_t stream
    device, written to caller buffers so that one launch serves every layer of a decode step, whose layers share one
    mask, and the per-layer calls pass seq_lens / kv_start. Inverts the reference's mask construction from pad_lens
    and the position (third_party/breeze-tts/models/cudagraph/backbone_graph.py:239-252), which its attention
-   re-reads per layer to skip masked chunks (flash/csrc/bb_attn.cu:102-140). mask: bz_mask_dtype BF16 or F32, row b
+   re-reads per layer to skip masked chunks (flash/csrc/bb_attn.cu:111-117). mask: bz_mask_dtype BF16 or F32, row b
    at mask + b*mask_stride_b (0 broadcasts one row); seq_lens, kv_start: int32 [batch] device arrays. */
 int bz_mask_interval(const void* mask, int32_t mask_dtype, int64_t mask_stride_b, int32_t batch, int32_t capacity,
                      int32_t* seq_lens, int32_t* kv_start, hipStream_t stream);
