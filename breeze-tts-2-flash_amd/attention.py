@@ -173,6 +173,24 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
     return out
 
 
+def gqa_decode_wave(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
+                    scale: float, out: torch.Tensor | None = None, *,
+                    kv_start: torch.Tensor | None = None) -> torch.Tensor:
+    """gqa_decode computed by one wave per (row, token, kv head) (bz_gqa_decode_wave: the device function attend_wave
+    launched alone; no split, no workspace). Same shapes and ranges as gqa_decode (no mask); out must be 16-byte
+    aligned with strides that are multiples of 8 elements. Slower than gqa_decode as a standalone op: it exists to
+    test the device function a whole-step depth kernel would call."""
+    a, out = _fill_args(q, k_cache, v_cache, scale, out, 0, 0, "auto")
+    dev = q.device
+    a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
+    a.kv_start = _int32_rows(kv_start, a.batch, "kv_start", dev).data_ptr() if kv_start is not None else None
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        kernels.check(kernels.load().bz_gqa_decode_wave(ctypes.byref(a), ctypes.c_void_p(stream)),
+                      "bz_gqa_decode_wave")
+    return out
+
+
 def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, mask: torch.Tensor,
                       scale: float, out: torch.Tensor | None = None, *, num_splits: int = 0, max_seq_len: int = 0,
                       combine: str | int = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:

@@ -9,6 +9,7 @@
 
 #include "bz_gqa_decode.h"
 #include "gqa_kernels.cuh"
+#include "gqa_wave.cuh"
 
 namespace {
 
@@ -25,6 +26,17 @@ SplitFn pick_combine(int D, int G) {
   BZ_COMBINE_CASE(128, 1) BZ_COMBINE_CASE(128, 2) BZ_COMBINE_CASE(128, 4) BZ_COMBINE_CASE(128, 8)
   BZ_COMBINE_CASE(64, 1) BZ_COMBINE_CASE(64, 2) BZ_COMBINE_CASE(64, 4) BZ_COMBINE_CASE(64, 8)
 #undef BZ_COMBINE_CASE
+  return nullptr;
+}
+
+using WaveFn = void (*)(const Params, int);
+
+WaveFn pick_wave(int D, int G) {
+#define BZ_WAVE_CASE(DD, GG) \
+  if (D == DD && G == GG) return gqa_wave_kernel<DD, GG>;
+  BZ_WAVE_CASE(128, 1) BZ_WAVE_CASE(128, 2) BZ_WAVE_CASE(128, 4) BZ_WAVE_CASE(128, 8)
+  BZ_WAVE_CASE(64, 1) BZ_WAVE_CASE(64, 2) BZ_WAVE_CASE(64, 4) BZ_WAVE_CASE(64, 8)
+#undef BZ_WAVE_CASE
   return nullptr;
 }
 
@@ -132,12 +144,42 @@ int resolve_splits(const bz_gqa_decode_args* a, int* splits) {
   return BZ_OK;
 }
 
+// The kernel parameters every entry shares: pointers, strides, sizes and the rows' range arrays.
+Params base_params(const bz_gqa_decode_args* a, const int32_t* seq_lens, const int32_t* kv_start) {
+  Params p{};
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.q_sb = a->q_stride_b;
+  p.q_sh = a->q_stride_h;
+  p.q_st = a->q_stride_t;
+  p.T = tokens_of(a);
+  p.k = static_cast<const uint16_t*>(a->k_cache);
+  p.v = static_cast<const uint16_t*>(a->v_cache);
+  p.kv_sb = a->kv_stride_b;
+  p.kv_sh = a->kv_stride_h;
+  p.kv_ss = a->kv_stride_s;
+  p.seq_lens = seq_lens;
+  p.kv_start = kv_start;
+  p.mask = a->mask;
+  p.m_sb = a->mask_stride_b;
+  p.scale_log2 = a->scale * kLog2e;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.o_sb = a->out_stride_b;
+  p.o_sh = a->out_stride_h;
+  p.o_st = a->out_stride_t;
+  p.B = a->batch;
+  p.NH = a->num_q_heads;
+  p.NKV = a->num_kv_heads;
+  p.cap = a->capacity;
+  p.splits = 1;
+  return p;
+}
+
 // Checks the workspace, picks the kernels and launches the split kernel (and, on request, the merge kernel).
 // f != nullptr selects the fused-prologue variant.
 int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
            int mask_kind, const bz_gqa_decode_fused_args* f) {
-  const int B = a->batch, NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
-  const int G = NH / NKV, T = tokens_of(a), R = rows_of(a);
+  const int NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
+  const int G = NH / NKV, R = rows_of(a);
   int splits = 0;
   int rc = resolve_splits(a, &splits);
   if (rc != BZ_OK) return rc;
@@ -160,30 +202,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
 
   char* wsb = static_cast<char*>(a->workspace);
-  Params p;
-  p.q = static_cast<const uint16_t*>(a->q);
-  p.q_sb = a->q_stride_b;
-  p.q_sh = a->q_stride_h;
-  p.q_st = a->q_stride_t;
-  p.T = T;
-  p.k = static_cast<const uint16_t*>(a->k_cache);
-  p.v = static_cast<const uint16_t*>(a->v_cache);
-  p.kv_sb = a->kv_stride_b;
-  p.kv_sh = a->kv_stride_h;
-  p.kv_ss = a->kv_stride_s;
-  p.seq_lens = seq_lens;
-  p.kv_start = kv_start;
-  p.mask = a->mask;
-  p.m_sb = a->mask_stride_b;
-  p.scale_log2 = a->scale * kLog2e;
-  p.out = static_cast<uint16_t*>(a->out);
-  p.o_sb = a->out_stride_b;
-  p.o_sh = a->out_stride_h;
-  p.o_st = a->out_stride_t;
-  p.B = B;
-  p.NH = NH;
-  p.NKV = NKV;
-  p.cap = cap;
+  Params p = base_params(a, seq_lens, kv_start);
   p.splits = splits;
   p.min_chunk = min_chunk;
   const bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
@@ -320,6 +339,23 @@ __attribute__((visibility("default"))) int bz_gqa_decode_fused(const bz_gqa_deco
   rc = mask_ranges(a, stream, &start, &end);
   if (rc != BZ_OK) return rc;
   return launch(a, stream, end, start, a->mask_dtype, f);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_wave(const bz_gqa_decode_args* a, hipStream_t stream) {
+  int rc = check_common(a, true);
+  if (rc != BZ_OK) return rc;
+  if (a->seq_lens == nullptr) return BZ_ERR_NULL;
+  if (a->mask != nullptr) return BZ_ERR_UNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(a->out) & 15) || ((a->out_stride_b | a->out_stride_h) & 7) ||
+      (tokens_of(a) > 1 && (a->out_stride_t & 7)))
+    return BZ_ERR_ALIGNMENT;
+  const WaveFn fn = pick_wave(a->head_dim, a->num_q_heads / a->num_kv_heads);
+  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
+  const Params p = base_params(a, a->seq_lens, a->kv_start);
+  const int groups = rows_of(a) * a->num_kv_heads;
+  constexpr int kWavesPerBlock = 256 / kWave;
+  hipLaunchKernelGGL(fn, dim3((groups + kWavesPerBlock - 1) / kWavesPerBlock), dim3(256), 0, stream, p, groups);
+  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
 __attribute__((visibility("default"))) int bz_mask_interval(const void* mask, int32_t mask_dtype,

@@ -23,20 +23,20 @@ INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libbz_gqa_decode.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 SOURCES = ["gqa_decode.hip", "gqa_fused.hip", "gemv.hip"]  # translation units, compiled in parallel
-HEADERS = ["gqa_kernels.cuh", "device_common.cuh"]
+HEADERS = ["gqa_kernels.cuh", "gqa_wave.cuh", "device_common.cuh"]
 ARCH = "gfx950"
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32)
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
     "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_fused", "bz_gqa_decode_workspace_size",
     "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version", "bz_gemv", "bz_rmsnorm",
-    "bz_mask_interval",
+    "bz_mask_interval", "bz_gqa_decode_wave",
 )
 
 MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
@@ -157,6 +157,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_mask_interval.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     lib.bz_mask_interval.restype = ctypes.c_int
+    lib.bz_gqa_decode_wave.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p]
+    lib.bz_gqa_decode_wave.restype = ctypes.c_int
 
 
 def load() -> ctypes.CDLL:

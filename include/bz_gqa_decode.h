@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 5
+#define BZ_GQA_DECODE_ABI_VERSION 6
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -150,6 +150,16 @@ typedef struct bz_gqa_decode_fused_args {
    Replaces attn_decode_fused (flash/csrc/bb_attn.cu:433-460, prologue :78-149, pybind :466-469), the entry the
    reference's decode step calls (flash/backbone.py:123-124). */
 int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* args, hipStream_t stream);
+
+/* The same attention as bz_gqa_decode (seq_lens / kv_start ranges, tokens_per_row causal tokens), computed by one
+   wave per (row, token, kv head) with no split, no workspace and no barrier. The wave's work is the device function
+   attend_wave (breeze-tts-2-flash_amd/csrc/gqa_wave.cuh), the attention stage for a kernel that runs a whole depth
+   decode step in one launch, as the reference's depth megakernel does (flash/csrc/depth_frame.cu:208-272, at most 17
+   positions per step); this entry launches it alone, so that it is tested and timed through the C ABI. As a
+   standalone launch it is slower than bz_gqa_decode, whose workgroup spreads a short row over four waves: one wave
+   runs the row's arithmetic serially. No mask (BZ_ERR_UNSUPPORTED); out and its strides 16-byte aligned;
+   workspace, num_splits, max_seq_len and combine are ignored; any row length works. */
+int bz_gqa_decode_wave(const bz_gqa_decode_args* args, hipStream_t stream);
 
 /* Per row b, the interval [kv_start[b], seq_lens[b]) of positions p < capacity whose additive mask value is > -1e30
    ([0, 0) for a row with none): the range bz_gqa_decode_masked and the mask form of bz_gqa_decode_fused derive on the
