@@ -136,6 +136,22 @@ __device__ __forceinline__ uint4 x_chunk(const GemvParams& p, const Rsrc& rx, in
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
 }
 
+// The residual values the writing lanes of a wave need (lane 16 q writes flat value 4 g + q of each group g, i.e.
+// output row r = f / M of batch row m = f % M), loaded with the first weight tiles so that the epilogue waits for
+// nothing: one 2-byte buffer load per group and lane. Values past the output rows are never used; loads past the
+// residual matrix read 0 without a memory access.
+template <int M, int R>
+__device__ __forceinline__ void load_residual(const GemvParams& p, int row0, int lane, float (&res)[(R * M + 3) / 4]) {
+  const Rsrc rr = span_rsrc(p.res, (int)(((int64_t)(M - 1) * p.ldr + p.ntot) * 2));
+  const int q = lane / 16;
+#pragma unroll
+  for (int g = 0; g < (R * M + 3) / 4; ++g) {
+    const int f = 4 * g + q, r = f / M, m = f % M;
+    const uint32_t off = (uint32_t)(((int64_t)m * p.ldr + row0 + r) * 2);
+    res[g] = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rr, off, 0, 0));
+  }
+}
+
 // KC > 0: x held in registers, KC chunks per lane (k <= 512 KC <= 2 tiles): no LDS, and the RMSNorm's sum of squares
 // is reduced over the wave, so the prologue needs no barrier. KC == 0: x staged in LDS (any k).
 template <int M, int R, bool NORM, int EPI, int KC>
@@ -174,6 +190,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) 
     }
   };
   const Rsrc rx = span_rsrc(p.x, (int)(((int64_t)(M - 1) * p.ldx + p.k) * 2));
+  [[maybe_unused]] float resv[(R * M + 3) / 4];
   float acc[NR][M];
 #pragma unroll
   for (int r = 0; r < NR; ++r)
@@ -202,6 +219,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) 
     }
     load(ta, 0);
     load(tb, 1);
+    if (EPI == BZ_GEMV_RESIDUAL) load_residual<M, R>(p, row0, lane, resv);
     __builtin_amdgcn_sched_barrier(0);
     if (NORM) {
 #pragma unroll
@@ -243,6 +261,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) 
     x_issue<M>(p, rx, xr);
     load(ta, 0);
     load(tb, 1);
+    if (EPI == BZ_GEMV_RESIDUAL) load_residual<M, R>(p, row0, lane, resv);
     __builtin_amdgcn_sched_barrier(0);
 
     stage_x<M, NORM>(p, rx, xr, xs);
@@ -300,7 +319,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) 
     if (EPI == BZ_GEMV_PLAIN) {
       v = red[g];
     } else if (EPI == BZ_GEMV_RESIDUAL) {
-      v = bf16_to_f32(p.res[(int64_t)m * p.ldr + n]) + bf16_to_f32(f32_to_bf16(red[g]));
+      v = resv[g] + bf16_to_f32(f32_to_bf16(red[g]));
     } else {
       const float gt = bf16_to_f32(f32_to_bf16(red[g]));
       const float up = bf16_to_f32(f32_to_bf16(red[NG / 4 + g]));
@@ -440,6 +459,8 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   const size_t lds = (size_t)a->m * kp * 2;
   if (lds > (size_t)kMaxLds || (int64_t)a->k * 2 > INT32_MAX) return BZ_ERR_UNSUPPORTED;
   if (((int64_t)(a->m - 1) * a->x_stride + a->k) * 2 > INT32_MAX) return BZ_ERR_SHAPE;  // x: 32-bit byte offsets
+  if (a->epilogue == BZ_GEMV_RESIDUAL && ((int64_t)(a->m - 1) * a->res_stride + ntot) * 2 > INT32_MAX)
+    return BZ_ERR_SHAPE;  // the residual: 32-bit byte offsets
 
   const int kc = kc_for(a->m, a->k);
   const int r = rows_per_wave(ntot, a->epilogue, kc);
