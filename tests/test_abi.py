@@ -256,3 +256,31 @@ def test_rmsnorm_validation(lib):
     assert lib.bz_rmsnorm(P, 1024, P, 1e-6, P, 2048, 2, 2048, None) == -2
     assert lib.bz_rmsnorm(P + 2, 2048, P, 1e-6, P, 2048, 2, 2048, None) == -4
     assert lib.bz_rmsnorm(P, 2048, P, 1e-6, P, 2052, 2, 2048, None) == -4
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), -1), (dict(seq_lens=None), -1), (dict(head_dim=96), -3), (dict(num_kv_heads=3), -2),
+    (dict(mask=0x50000, mask_dtype=1), -3),                         # the wave entry takes no mask
+    (dict(out=0x40008), -4), (dict(out_stride_h=132), -4), (dict(out_stride_b=16 * 128 + 4), -4),
+    (dict(tokens_per_row=2, q_stride_t=128 * 16, out_stride_t=68), -4),
+    (dict(k_cache=0x100008), -4),
+])
+def test_wave_validation(lib, K, over, code):
+    a = _good_args(K, **over)
+    assert lib.bz_gqa_decode_wave(ctypes.byref(a), None) == code
+    assert lib.bz_gqa_decode_wave(None, None) == -1
+
+
+def test_mask_interval_validation(lib, K):
+    f = lib.bz_mask_interval
+    ok = (0x50000, K.MASK_BF16, 2048, 2, 2048, 0x60000, 0x60010, None)
+    for i, bad, code in [(0, None, -1), (5, None, -1), (6, None, -1),          # null mask / outputs
+                         (1, K.MASK_NONE, -6), (1, 7, -6),                     # mask dtype
+                         (3, 0, -2), (4, 0, -2), (2, -1, -2), (2, 100, -2),    # batch, capacity, row stride
+                         (0, 0x50001, -4), (5, 0x60002, -4)]:                  # alignment
+        args = list(ok)
+        args[i] = bad
+        assert f(*args) == code, (i, bad)
+    args = list(ok)
+    args[1], args[0] = K.MASK_F32, 0x50002
+    assert f(*args) == -4                                                     # fp32 mask needs 4-byte alignment
