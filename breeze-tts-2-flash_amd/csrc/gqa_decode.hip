@@ -15,8 +15,9 @@ namespace {
 
 SplitFn pick_split(int D, int G, int mk, int ppt, int nt, bool fused) {
   if (fused) return bz::pick_split_fused(D, G, mk, ppt, nt);
-  if (D == 128) return nt == 512 ? pick_group<128, 512, false>(G, mk, ppt) : pick_group<128, 256, false>(G, mk, ppt);
-  if (D == 64) return nt == 512 ? pick_group<64, 512, false>(G, mk, ppt) : pick_group<64, 256, false>(G, mk, ppt);
+  if (nt != kSplitThreads) return nullptr;
+  if (D == 128) return pick_group<128, kSplitThreads, false>(G, mk, ppt);
+  if (D == 64) return pick_group<64, kSplitThreads, false>(G, mk, ppt);
   return nullptr;
 }
 
@@ -55,13 +56,6 @@ int ppt_for(int D, int G, int chunk, int nt) {
   return 2 * rows >= chunk ? 1 : 2;
 }
 
-// Threads per split workgroup: 512 (8 waves, two per SIMD, so one wave's VALU latency hides behind the other's)
-// when the grid has at most one workgroup per CU and the chunk fills a 512-thread tile; 256 otherwise (more
-// workgroups already give each SIMD several waves), and for G = 8, whose accumulators need the registers.
-int threads_for(int D, int G, int chunk, int64_t workgroups, int cus) {
-  if (G >= 8 || workgroups > cus) return 256;
-  return chunk >= 512 / (D / 8) ? 512 : 256;
-}
 
 std::atomic<int> g_cu_count[kMaxDevices];
 
@@ -192,10 +186,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   const int len = effective_len(cap, a->max_seq_len);
   int chunk = (len + splits - 1) / splits;
   if (chunk < min_chunk) chunk = min_chunk;
-  int cus = 0;
-  rc = device_cus(&cus);
-  if (rc != BZ_OK) return rc;
-  const int nt = threads_for(D, G, chunk, (int64_t)splits * NKV * R, cus);
+  const int nt = kSplitThreads;
   const int ppt = ppt_for(D, G, chunk, nt);
   SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt, f != nullptr);
   SplitFn comb_fn = pick_combine(D, G);

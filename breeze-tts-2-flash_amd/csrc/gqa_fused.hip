@@ -6,8 +6,8 @@
 namespace bz {
 
 SplitFn pick_split_fused(int D, int G, int mk, int ppt, int nt) {
-  if (D != 128) return nullptr;
-  return nt == 512 ? pick_group<128, 512, true>(G, mk, ppt) : pick_group<128, 256, true>(G, mk, ppt);
+  if (D != 128 || nt != kSplitThreads) return nullptr;
+  return pick_group<128, kSplitThreads, true>(G, mk, ppt);
 }
 
 }  // namespace bz

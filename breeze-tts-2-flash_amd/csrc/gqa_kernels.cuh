@@ -9,7 +9,7 @@
 // the eager bf16 rounding points, and writes the new k and v into cache slot cache_pos.
 //
 // Work decomposition (split-K over the KV length, "flash-decoding"):
-//   grid (splits, num_kv_heads, batch), NT = 256 or 512 threads (4 or 8 wave64) per workgroup.
+//   grid (splits, num_kv_heads, batch), NT = 256 threads (4 wave64) per workgroup.
 //   Each row's valid length is cut on the device into nact <= splits chunks of
 //   chunk = max(min_chunk, ceil(len / splits)) positions, so a fixed grid serves every length (HIP-graph safe) and
 //   the work follows the real length: workgroups past nact exit at once.
@@ -82,6 +82,9 @@ using bz::SplitFn;
 
 
 constexpr int kThreads = 256;  // 4 wave64 (merge and mask kernels)
+// Threads per split workgroup: four waves. Eight (two per SIMD, one workgroup per CU at B = 2) measured slower once
+// the loads, reductions and merge took their present form: config 2 6.45 against 6.39 us, config 3 9.84 against 9.62.
+constexpr int kSplitThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxSplits = 256;
 constexpr int kMaxDevices = 64;
@@ -665,8 +668,7 @@ SplitFn pick_group(int G, int mk, int ppt) {
     case 1: return pick_mask<D, 1, NT, FUSED>(mk, ppt);
     case 2: return pick_mask<D, 2, NT, FUSED>(mk, ppt);
     case 4: return pick_mask<D, 4, NT, FUSED>(mk, ppt);
-    // G = 8 runs with 256 threads only (the host never picks 512 for it: its accumulators would not fit in VGPRs)
-    case 8: if constexpr (NT == 256) return pick_mask<D, 8, NT, FUSED>(mk, ppt); else return nullptr;
+    case 8: return pick_mask<D, 8, NT, FUSED>(mk, ppt);
     default: return nullptr;
   }
 }
