@@ -284,3 +284,21 @@ def test_mask_interval_validation(lib, K):
     args = list(ok)
     args[1], args[0] = K.MASK_F32, 0x50002
     assert f(*args) == -4                                                     # fp32 mask needs 4-byte alignment
+
+
+def test_missing_library_fails_loudly(K, tmp_path, monkeypatch):
+    """No build, no fallback: load() and every entry that needs the library raise."""
+    from breeze_tts_2_flash_amd import backbone
+
+    monkeypatch.setattr(K, "_LIB", None)
+    monkeypatch.setattr(K, "LIB_PATH", tmp_path / "libbz_gqa_decode.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        K.load()
+
+    class Graph:
+        def _decode_step(self):
+            pass
+
+    with pytest.raises(RuntimeError, match="missing"):
+        backbone.install(Graph)
+    assert Graph._decode_step is not backbone.fused_decode_step
