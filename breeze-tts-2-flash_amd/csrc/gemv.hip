@@ -26,8 +26,13 @@
 
 namespace {
 
-constexpr int kGemvThreads = 256;              // 4 waves per workgroup
+constexpr int kGemvThreads = 256;              // 4 waves per workgroup (x in registers; rmsnorm)
 constexpr int kGemvWaves = kGemvThreads / kWave;
+// Threads of a workgroup that stages x in LDS: eight waves share one copy of x (down: 6.47 against 6.9 us with
+// four); with x in registers every wave loads its own, and four waves per workgroup measured fastest.
+constexpr int kGemvLdsThreads = 512;
+template <int KC>
+constexpr int gemv_threads() { return KC > 0 ? kGemvThreads : kGemvLdsThreads; }
 constexpr int kChunk = 8 * kWave;              // k elements per wave load instruction
 constexpr int kU = 2;                          // chunks per tile
 constexpr int kTileK = kChunk * kU;            // k elements per tile
@@ -65,13 +70,13 @@ __device__ __forceinline__ uint4 x_vector(const GemvParams& p, const Rsrc& rx, i
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
 }
 
-template <int M>
+template <int M, int NT>
 __device__ __forceinline__ void x_issue(const GemvParams& p, const Rsrc& rx, uint4 (&xr)[kXr]) {
 #pragma unroll
-  for (int i = 0; i < kXr; ++i) xr[i] = x_vector<M>(p, rx, threadIdx.x + i * kGemvThreads);
+  for (int i = 0; i < kXr; ++i) xr[i] = x_vector<M>(p, rx, threadIdx.x + i * NT);
 }
 
-template <int M, bool NORM>
+template <int M, bool NORM, int NT>
 __device__ __forceinline__ void stage_x(const GemvParams& p, const Rsrc& rx, const uint4 (&xr)[kXr], uint16_t* xs) {
   const int tid = threadIdx.x;
   const int kv = p.kp / 8, total = M * kv;
@@ -94,12 +99,12 @@ __device__ __forceinline__ void stage_x(const GemvParams& p, const Rsrc& rx, con
   };
 #pragma unroll
   for (int i = 0; i < kXr; ++i) {
-    const int idx = tid + i * kGemvThreads;
+    const int idx = tid + i * NT;
     if (idx < total) put(idx, xr[i]);
   }
-  for (int idx = tid + kXr * kGemvThreads; idx < total; idx += kGemvThreads) put(idx, x_vector<M>(p, rx, idx));
+  for (int idx = tid + kXr * NT; idx < total; idx += NT) put(idx, x_vector<M>(p, rx, idx));
   if (!NORM) return;
-  __shared__ float red[kGemvWaves][M];
+  __shared__ float red[NT / kWave][M];
   const int lane = tid % kWave, wave = tid / kWave;
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -112,9 +117,9 @@ __device__ __forceinline__ void stage_x(const GemvParams& p, const Rsrc& rx, con
   for (int m = 0; m < M; ++m) {
     float tot = 0.f;
 #pragma unroll
-    for (int w = 0; w < kGemvWaves; ++w) tot += red[w][m];
+    for (int w = 0; w < NT / kWave; ++w) tot += red[w][m];
     const float r = rsqrtf(tot * (1.f / (float)p.k) + p.eps);
-    for (int j = tid; j < kv; j += kGemvThreads) {
+    for (int j = tid; j < kv; j += NT) {
       float f[8], w[8];
       unpack8(reinterpret_cast<const uint4*>(xs + m * p.kp)[j], f);
       unpack8(__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, j * 16, 0, 0)), w);
@@ -155,11 +160,12 @@ __device__ __forceinline__ void load_residual(const GemvParams& p, int row0, int
 // KC > 0: x held in registers, KC chunks per lane (k <= 512 KC <= 2 tiles): no LDS, and the RMSNorm's sum of squares
 // is reduced over the wave, so the prologue needs no barrier. KC == 0: x staged in LDS (any k).
 template <int M, int R, bool NORM, int EPI, int KC>
-__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) {
+__global__ void __launch_bounds__(gemv_threads<KC>()) gemv_kernel(const GemvParams p) {
+  constexpr int NT = gemv_threads<KC>(), NW = NT / kWave;
   constexpr int NR = EPI == BZ_GEMV_SILU_MUL ? 2 * R : R;  // weight rows per wave
   extern __shared__ __align__(16) uint16_t xs[];            // [M][kp] bf16
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+  const int row0 = (blockIdx.x * NW + wave) * R;
 
   // this wave's weight rows (a row past the last output: an empty resource, whose loads read 0)
   Rsrc wr[NR];
@@ -258,13 +264,13 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const GemvParams p) 
   } else {
     // x first (the prologue then waits for x alone), then the first two weight tiles, all before the prologue
     uint4 xr[kXr];
-    x_issue<M>(p, rx, xr);
+    x_issue<M, NT>(p, rx, xr);
     load(ta, 0);
     load(tb, 1);
     if (EPI == BZ_GEMV_RESIDUAL) load_residual<M, R>(p, row0, lane, resv);
     __builtin_amdgcn_sched_barrier(0);
 
-    stage_x<M, NORM>(p, rx, xr, xs);
+    stage_x<M, NORM, NT>(p, rx, xr, xs);
     __syncthreads();
 
     auto consume = [&](const uint4 (&t)[NR][kU], int it) {
@@ -483,9 +489,10 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   p.ldy = a->y_stride;
   p.res = static_cast<const uint16_t*>(a->res);
   p.ldr = a->res_stride;
-  const int rows_per_block = kGemvWaves * r;
+  const int threads = kc > 0 ? kGemvThreads : kGemvLdsThreads;
+  const int rows_per_block = threads / kWave * r;
   const int grid = (ntot + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(kGemvThreads), kc > 0 ? 0 : lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), kc > 0 ? 0 : lds, stream, p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
