@@ -395,3 +395,16 @@ def test_concurrent_streams_and_threads(device):
     assert not errors, errors
     for i in range(2):
         assert_close(outs[i], oracle(cases[i][0]), f"stream {i}")
+
+
+@pytest.mark.parametrize("splits", [0, 1, 7, 256])
+def test_long_context(device, splits):
+    """A 32768-slot cache: a full row and a left-padded partial one, the default split count (chunks capped at 256
+    positions), one workgroup streaming 32768 positions in 512 tiles, a ragged 7-way split, and the largest split
+    count (256)."""
+    lens, starts = [32768, 20001], [0, 5]
+    w, st = rand_case(31 + splits, 2, 16, 8, 128, 32768, lens, starts)
+    g = w.to(device)
+    out = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=splits)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu(), oracle(w, kv_start=st), f"long context splits={splits}")
