@@ -438,16 +438,16 @@ def main():
             print(f"[bench] {k}: {v}", file=sys.stderr, flush=True)
         line["extra"] = extra
     if not args.no_cpu:
-        us_cpu, cores, n = cpu_baseline(w2, budget_s=30.0)
+        us_cpu, cores, n = cpu_baseline(w2, calls=100000, budget_s=10.0)
         line["cpu_baseline"] = {"value": round(nbytes / us_cpu / 1e3, 3), "unit": "GB/s", "cores": cores,
                                 "kind": "port", "us_per_call": round(us_cpu, 1),
                                 "sample": f"config {cfg} inputs, the reference's eager bf16 chain over the full "
                                           f"{w2.capacity}-slot cache with the interval mask, median of {n} calls "
-                                          f"after 20 warmups"}
+                                          f"(10 s of CPU time) after 20 warmups"}
         print(f"[bench] cpu baseline: {us_cpu:.1f} us/call on {cores} threads", file=sys.stderr, flush=True)
         # beside it: the reference's own CPU-runnable case (config 1) and the fp32 SDPA oracle on the headline inputs
-        us_c1, _, n1 = cpu_baseline(workloads.make(1), kind="eager", budget_s=5.0)
-        us_sd, _, nsd = cpu_baseline(w2, kind="sdpa", calls=50, warmup=5, budget_s=5.0)
+        us_c1, _, n1 = cpu_baseline(workloads.make(1), kind="eager", calls=100000, budget_s=3.0)
+        us_sd, _, nsd = cpu_baseline(w2, kind="sdpa", calls=100000, warmup=5, budget_s=3.0)
         line["cpu_baseline"]["extra"] = {
             "config1_eager_us_per_call": round(us_c1, 1), "config1_calls": n1,
             f"config{cfg}_sdpa_fp32_us_per_call": round(us_sd, 1), f"config{cfg}_sdpa_calls": nsd}
