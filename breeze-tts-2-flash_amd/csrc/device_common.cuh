@@ -15,6 +15,21 @@ constexpr int kWave = 64;
 constexpr int kStream = 2;
 constexpr int kSc1 = 16;
 
+// The first active lane's value, in a scalar register. For values that are wave-uniform but that the compiler cannot
+// prove so (anything derived from threadIdx.x / kWave): a buffer resource built from a value the compiler takes for
+// divergent is held in VGPRs, and every load through it becomes a loop over the distinct resources of the wave
+// (v_readfirstlane, compare, exec mask, branch per load instruction).
+__device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t wave_uniform(int64_t x) {
+  const uint64_t u = (uint64_t)x;
+  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u));
+}
+template <class T>
+__device__ __forceinline__ T* wave_uniform(T* ptr) {
+  return reinterpret_cast<T*>(wave_uniform(reinterpret_cast<int64_t>(ptr)));
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }

@@ -37,6 +37,10 @@ constexpr int kChunk = 8 * kWave;              // k elements per wave load instr
 constexpr int kU = 2;                          // chunks per tile
 constexpr int kTileK = kChunk * kU;            // k elements per tile
 constexpr int kMaxLds = 64 * 1024;             // bytes of LDS for x
+// With x in registers every wave issues all its weight loads at once; spacing them by s_sleep(kIssueGap) (about
+// 64 * kIssueGap clocks) measured faster: q|k|v 5.06 against 5.19 us, gate/up 10.0 against 10.3-10.5. Gaps of 1, 3, 4
+// and 6 were tried; 2 was best or within noise of best.
+constexpr int kIssueGap = 2;
 
 struct GemvParams {
   const uint16_t* x;
@@ -164,7 +168,11 @@ __global__ void __launch_bounds__(gemv_threads<KC>()) gemv_kernel(const GemvPara
   constexpr int NT = gemv_threads<KC>(), NW = NT / kWave;
   constexpr int NR = EPI == BZ_GEMV_SILU_MUL ? 2 * R : R;  // weight rows per wave
   extern __shared__ __align__(16) uint16_t xs[];            // [M][kp] bf16
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  // With x in registers the wave index goes through a scalar register, so the weight resources are scalar and each
+  // load is one instruction. The LDS path leaves it in a VGPR, where the compiler issues every load from a
+  // one-iteration loop over the wave's distinct resources: measured faster there (down: 6.03 against 6.36 us with
+  // scalar resources, with or without pacing), for reasons not pinned down.
+  const int tid = threadIdx.x, lane = tid % kWave, wave = KC > 0 ? wave_uniform(tid / kWave) : tid / kWave;
   const int row0 = (blockIdx.x * NW + wave) * R;
 
   // this wave's weight rows (a row past the last output: an empty resource, whose loads read 0)
@@ -191,8 +199,10 @@ __global__ void __launch_bounds__(gemv_threads<KC>()) gemv_kernel(const GemvPara
     for (int u = 0; u < kU; ++u) {
       const uint32_t off = (uint32_t)(it * kTileK + u * kChunk) * 2 + lane_off;
 #pragma unroll
-      for (int r = 0; r < NR; ++r)
+      for (int r = 0; r < NR; ++r) {
         t[r][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr[r], off, 0, kStream));
+        if constexpr (KC > 0) __builtin_amdgcn_s_sleep(kIssueGap);
+      }
     }
   };
   const Rsrc rx = span_rsrc(p.x, (int)(((int64_t)(M - 1) * p.ldx + p.k) * 2));

@@ -46,20 +46,24 @@ __device__ void attend_wave(const WaveAttention& a) {
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   constexpr int LPR = D / 8, RPW = kWave / LPR, PPT = 2, TP = RPW * PPT;
   const int lane = __lane_id(), r = lane / LPR, c = lane % LPR;
-  const int start = a.start, end = a.end > a.start ? a.end : a.start;
+  // the arguments are wave-uniform; taking them through a scalar register keeps the buffer resources and the loop
+  // bounds scalar whatever the caller derived them from
+  const int start = wave_uniform(a.start), end = max(start, wave_uniform(a.end));
+  const int64_t q_sh = wave_uniform(a.q_sh), kv_ss = wave_uniform(a.kv_ss), o_sh = wave_uniform(a.o_sh);
+  uint16_t* const outp = wave_uniform(a.out);
 
   // q first: loads complete in issue order, so the first tile's q.k waits for q and that tile alone
-  const Rsrc rq = span_rsrc(a.q, (int)(((G - 1) * a.q_sh + D) * 2));
+  const Rsrc rq = span_rsrc(wave_uniform(a.q), (int)(((G - 1) * q_sh + D) * 2));
   uint4 qp[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qp[g] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)((g * a.q_sh + 8 * c) * 2),
+    qp[g] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)((g * q_sh + 8 * c) * 2),
                                                                             0, 0));
   Spans sp;
-  sp.row_bytes = (uint32_t)a.kv_ss * 2;
+  sp.row_bytes = (uint32_t)kv_ss * 2;
   sp.lane_off = 16 * c;
-  sp.k = span_rsrc(a.k, end * (int)sp.row_bytes);
-  sp.v = span_rsrc(a.v, end * (int)sp.row_bytes);
+  sp.k = span_rsrc(wave_uniform(a.k), end * (int)sp.row_bytes);
+  sp.v = span_rsrc(wave_uniform(a.v), end * (int)sp.row_bytes);
   Tile<PPT> ta, tb;
   load_tile<RPW, PPT, BZ_MASK_NONE>(ta, sp, start + r);
   load_tile<RPW, PPT, BZ_MASK_NONE>(tb, sp, start + TP + r);
@@ -98,7 +102,7 @@ __device__ void attend_wave(const WaveAttention& a) {
       w.y = pack_bf16x2(o[2], o[3]);
       w.z = pack_bf16x2(o[4], o[5]);
       w.w = pack_bf16x2(o[6], o[7]);
-      *reinterpret_cast<uint4*>(a.out + g * a.o_sh + 8 * c) = w;
+      *reinterpret_cast<uint4*>(outp + g * o_sh + 8 * c) = w;
     }
   }
 }
@@ -107,7 +111,7 @@ __device__ void attend_wave(const WaveAttention& a) {
 // to itself), then attend_wave. Four waves per workgroup; waves past the last group exit (wave-uniform).
 template <int D, int G>
 __global__ void __launch_bounds__(256) gqa_wave_kernel(const bz::Params p, int groups) {
-  const int gi = blockIdx.x * (256 / kWave) + (int)(threadIdx.x / kWave);
+  const int gi = blockIdx.x * (256 / kWave) + wave_uniform((int)(threadIdx.x / kWave));
   if (gi >= groups) return;
   const int h = gi % p.NKV, z = gi / p.NKV;  // z = row * T + token
   const int b = z / p.T, tok = z - b * p.T;
