@@ -344,8 +344,7 @@ __attribute__((visibility("default"))) int bz_gqa_decode_wave(const bz_gqa_decod
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   const Params p = base_params(a, a->seq_lens, a->kv_start);
   const int groups = rows_of(a) * a->num_kv_heads;
-  constexpr int kWavesPerBlock = 256 / kWave;
-  hipLaunchKernelGGL(fn, dim3((groups + kWavesPerBlock - 1) / kWavesPerBlock), dim3(256), 0, stream, p, groups);
+  hipLaunchKernelGGL(fn, dim3(groups), dim3(kWave), 0, stream, p, groups);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
