@@ -240,7 +240,7 @@ def time_backbone(pkg, dev, steps):
 
 def time_depth_frame(pkg, dev, steps, warmup, wave=False):
     """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph; with
-    wave=True through bz_gqa_decode_wave (one wave per (row, kv head), no split) instead of the split kernel."""
+    wave=True through bz_gqa_decode_wave (one wave per (row, q head), no split) instead of the split kernel."""
     import torch
     from breeze_tts_2_flash_amd import workloads
 
@@ -431,7 +431,7 @@ def main():
         us_w, _ = time_depth_frame(pkg, dev, args.steps, args.warmup, wave=True)
         extra["config5_depth_frame_wave"] = {"us_per_frame": round(us_w, 3), "us_per_call": round(us_w / 32, 3),
                                              "bytes_per_frame": fb, "GB/s": round(fb / us_w / 1e3, 1)}
-        print(f"[bench] config 5 depth frame, one wave per group: {us_w:.3f} us/frame", file=sys.stderr, flush=True)
+        print(f"[bench] config 5 depth frame, one wave per (row, q head): {us_w:.3f} us/frame", file=sys.stderr, flush=True)
         bb = time_backbone(pkg, dev, args.steps)
         extra["backbone"] = bb
         for k, v in bb.items():

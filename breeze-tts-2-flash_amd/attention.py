@@ -176,10 +176,10 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
 def gqa_decode_wave(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
                     scale: float, out: torch.Tensor | None = None, *,
                     kv_start: torch.Tensor | None = None) -> torch.Tensor:
-    """gqa_decode computed by one wave per (row, token, kv head) (bz_gqa_decode_wave: the device function attend_wave
+    """gqa_decode computed by one wave per (row, token, q head) (bz_gqa_decode_wave: the device function attend_wave
     launched alone; no split, no workspace). Same shapes and ranges as gqa_decode (no mask); out must be 16-byte
-    aligned with strides that are multiples of 8 elements. Slower than gqa_decode as a standalone op: it exists to
-    test the device function a whole-step depth kernel would call."""
+    aligned with strides that are multiples of 8 elements. Faster than gqa_decode only on short rows already cached
+    (the real depth shape); it exists to test and time the device function a whole-step depth kernel would call."""
     a, out = _fill_args(q, k_cache, v_cache, scale, out, 0, 0, "auto")
     dev = q.device
     a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()

@@ -32,12 +32,9 @@ SplitFn pick_combine(int D, int G) {
 
 using WaveFn = void (*)(const Params, int);
 
-WaveFn pick_wave(int D, int G) {
-#define BZ_WAVE_CASE(DD, GG) \
-  if (D == DD && G == GG) return gqa_wave_kernel<DD, GG>;
-  BZ_WAVE_CASE(128, 1) BZ_WAVE_CASE(128, 2) BZ_WAVE_CASE(128, 4) BZ_WAVE_CASE(128, 8)
-  BZ_WAVE_CASE(64, 1) BZ_WAVE_CASE(64, 2) BZ_WAVE_CASE(64, 4) BZ_WAVE_CASE(64, 8)
-#undef BZ_WAVE_CASE
+WaveFn pick_wave(int D) {
+  if (D == 128) return gqa_wave_kernel<128>;
+  if (D == 64) return gqa_wave_kernel<64>;
   return nullptr;
 }
 
@@ -83,9 +80,14 @@ int effective_len(int capacity, int max_seq_len) {
 
 // Split count: enough workgroups to give every CU one (cus / units splits), and no chunk longer than kMaxChunk
 // positions even in the longest row (a chunk streams through one workgroup two tiles at a time, so its latency grows
-// with its length), but no split shorter than min_chunk positions.
+// with its length), but no split shorter than min_chunk positions. A row whose whole K+V span fits kOneSplitBytes is
+// not split: the cross-workgroup merge of two or more splits (partials stored, counted, reloaded) costs about 2 us,
+// more than one workgroup takes to stream 64 KB (cold, B2 16/8: head_dim 128, 128 positions 4.45 against 5.42 us;
+// head_dim 64, 256 positions 4.47 against 5.17; at 128 KB one split is slower: 6.23 against 5.47).
 int default_splits_for(int units, int D, int len, int cus) {
   constexpr int kMaxChunk = 256;
+  constexpr int64_t kOneSplitBytes = 64 * 1024;
+  if ((int64_t)len * 4 * D <= kOneSplitBytes) return 1;
   const int min_chunk = min_chunk_for(D);
   const int useful = len > 0 ? (len + min_chunk - 1) / min_chunk : 1;
   int s = (cus + units - 1) / units;
@@ -340,11 +342,11 @@ __attribute__((visibility("default"))) int bz_gqa_decode_wave(const bz_gqa_decod
   if ((reinterpret_cast<uintptr_t>(a->out) & 15) || ((a->out_stride_b | a->out_stride_h) & 7) ||
       (tokens_of(a) > 1 && (a->out_stride_t & 7)))
     return BZ_ERR_ALIGNMENT;
-  const WaveFn fn = pick_wave(a->head_dim, a->num_q_heads / a->num_kv_heads);
+  const WaveFn fn = pick_wave(a->head_dim);
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   const Params p = base_params(a, a->seq_lens, a->kv_start);
-  const int groups = rows_of(a) * a->num_kv_heads;
-  hipLaunchKernelGGL(fn, dim3(groups), dim3(kWave), 0, stream, p, groups);
+  const int waves = rows_of(a) * a->num_q_heads;
+  hipLaunchKernelGGL(fn, dim3(waves), dim3(kWave), 0, stream, p, waves);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

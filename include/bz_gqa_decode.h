@@ -152,13 +152,13 @@ typedef struct bz_gqa_decode_fused_args {
 int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* args, hipStream_t stream);
 
 /* The same attention as bz_gqa_decode (seq_lens / kv_start ranges, tokens_per_row causal tokens), computed by one
-   wave per (row, token, kv head) with no split, no workspace and no barrier. The wave's work is the device function
+   wave per (row, token, q head) with no split, no workspace and no barrier. The wave's work is the device function
    attend_wave (breeze-tts-2-flash_amd/csrc/gqa_wave.cuh), the attention stage for a kernel that runs a whole depth
    decode step in one launch, as the reference's depth megakernel does (flash/csrc/depth_frame.cu:208-272, at most 17
-   positions per step); this entry launches it alone, so that it is tested and timed through the C ABI. As a
-   standalone launch it is slower than bz_gqa_decode, whose workgroup spreads a short row over four waves: one wave
-   runs the row's arithmetic serially. No mask (BZ_ERR_UNSUPPORTED); out and its strides 16-byte aligned;
-   workspace, num_splits, max_seq_len and combine are ignored; any row length works. */
+   positions per step); this entry launches it alone, so that it is tested and timed through the C ABI. Each q head
+   reads its K/V itself, so it is faster than bz_gqa_decode only on short rows already in the cache hierarchy (the
+   real depth shape); on cold or long rows it is slower. No mask (BZ_ERR_UNSUPPORTED); out and its strides 16-byte
+   aligned; workspace, num_splits, max_seq_len and combine are ignored; any row length works. */
 int bz_gqa_decode_wave(const bz_gqa_decode_args* args, hipStream_t stream);
 
 /* Per row b, the interval [kv_start[b], seq_lens[b]) of positions p < capacity whose additive mask value is > -1e30

@@ -219,6 +219,28 @@ def test_split_count_invariance(device):
         assert np.abs(o - outs[1]).max() <= 2 * 2 ** -7 * max(1.0, np.abs(ref).max())
 
 
+@pytest.mark.parametrize("D,cap", [(128, 128), (128, 136), (64, 256), (64, 264)])
+def test_one_split_up_to_64_kib(device, D, cap):
+    """The default split count is 1 while a row's K+V span (cap x 4 D bytes) is at most 64 KiB, several above; either
+    way the default call matches the oracle and the explicit one-split call within tolerance."""
+    from breeze_tts_2_flash_amd import default_splits
+
+    one = cap * 4 * D <= 64 * 1024
+    assert (default_splits(2, 8, D, cap) == 1) == one
+    assert default_splits(16, 8, D, cap) == 1 or not one
+    w, st = rand_case(cap + D, 2, 16, 8, D, cap, [cap, cap - 3], starts=[0, 2])
+    g = w.to(device)
+    starts = st.to(device)
+    out = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=starts).float().cpu().numpy()
+    out1 = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=starts, num_splits=1).float().cpu().numpy()
+    torch.cuda.synchronize()
+    ref = oracle(w, kv_start=[0, 2])
+    assert_close(out, ref, f"D={D} cap={cap} default")
+    assert_close(out1, ref, f"D={D} cap={cap} one split")
+    if one:
+        assert np.array_equal(out, out1)
+
+
 # ---------------------------------------------------------------------------------------------- masks / compat
 
 @pytest.mark.parametrize("mdtype", [torch.bfloat16, torch.float32])
