@@ -170,7 +170,38 @@ Params base_params(const bz_gqa_decode_args* a, const int32_t* seq_lens, const i
   return p;
 }
 
-// Checks the workspace, picks the kernels and launches the split kernel (and, on request, the merge kernel).
+// One wave per (row, token, q head): the device function attend_wave launched alone (bz_gqa_decode_wave, and the
+// automatic route below). out and its strides must be 16-byte aligned.
+bool wave_out_aligned(const bz_gqa_decode_args* a) {
+  return !((reinterpret_cast<uintptr_t>(a->out) & 15) || ((a->out_stride_b | a->out_stride_h) & 7) ||
+           (tokens_of(a) > 1 && (a->out_stride_t & 7)));
+}
+
+int launch_wave(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start) {
+  const WaveFn fn = pick_wave(a->head_dim);
+  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
+  const Params p = base_params(a, seq_lens, kv_start);
+  const int waves = rows_of(a) * a->num_q_heads;
+  hipLaunchKernelGGL(fn, dim3(waves), dim3(kWave), 0, stream, p, waves);
+  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
+
+// The automatic route to the wave kernel: rows of at most kWaveRouteLen positions in groups of four or more q heads
+// (the reference's depth transformer: 8 q / 2 KV heads, at most 17 positions), with nothing asked explicitly (split
+// count, combine mode) and no mask. There the split kernel's waves each run the dot products and softmax of all G
+// heads in series, and one wave per q head is faster (B2 8/2 D128, per launch: lengths 2..17 2.9 against 3.8 us;
+// 32 positions 3.45 against 3.89 with the rows in the L2, as a depth step's freshly written rows are). Cold rows
+// would favour the split kernel (32 positions: 4.25 against 3.90 us), since each q head reads its K/V itself.
+constexpr int kWaveRouteLen = 32;
+
+bool wave_route(const bz_gqa_decode_args* a, int mask_kind, const bz_gqa_decode_fused_args* f) {
+  return f == nullptr && mask_kind == BZ_MASK_NONE && a->num_splits == 0 && a->combine == BZ_COMBINE_AUTO &&
+         a->num_q_heads >= 4 * a->num_kv_heads && effective_len(a->capacity, a->max_seq_len) <= kWaveRouteLen &&
+         wave_out_aligned(a);
+}
+
+// Checks the workspace, picks the kernels and launches the split kernel (and, on request, the merge kernel),
+// or the wave kernel where wave_route says so.
 // f != nullptr selects the fused-prologue variant.
 int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
            int mask_kind, const bz_gqa_decode_fused_args* f) {
@@ -183,6 +214,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   const WsLayout ws = ws_layout(R, NH, NKV, D, splits);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
+  if (wave_route(a, mask_kind, f)) return launch_wave(a, stream, seq_lens, kv_start);
 
   const int min_chunk = min_chunk_for(D);
   const int len = effective_len(cap, a->max_seq_len);
@@ -339,15 +371,8 @@ __attribute__((visibility("default"))) int bz_gqa_decode_wave(const bz_gqa_decod
   if (rc != BZ_OK) return rc;
   if (a->seq_lens == nullptr) return BZ_ERR_NULL;
   if (a->mask != nullptr) return BZ_ERR_UNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(a->out) & 15) || ((a->out_stride_b | a->out_stride_h) & 7) ||
-      (tokens_of(a) > 1 && (a->out_stride_t & 7)))
-    return BZ_ERR_ALIGNMENT;
-  const WaveFn fn = pick_wave(a->head_dim);
-  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
-  const Params p = base_params(a, a->seq_lens, a->kv_start);
-  const int waves = rows_of(a) * a->num_q_heads;
-  hipLaunchKernelGGL(fn, dim3(waves), dim3(kWave), 0, stream, p, waves);
-  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+  if (!wave_out_aligned(a)) return BZ_ERR_ALIGNMENT;
+  return launch_wave(a, stream, a->seq_lens, a->kv_start);
 }
 
 __attribute__((visibility("default"))) int bz_mask_interval(const void* mask, int32_t mask_dtype,

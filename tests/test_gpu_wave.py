@@ -140,3 +140,23 @@ def test_argument_errors(device):
         gqa_decode_wave(q, k, k, lens, 0.1, buf[1:].view(2, 16, 128))
     with pytest.raises(RuntimeError):  # head_dim 96
         gqa_decode_wave(q[..., :96].contiguous(), k[..., :96].contiguous(), k[..., :96].contiguous(), lens, 0.1)
+
+
+def test_gqa_decode_routes_short_wide_groups(device):
+    """bz_gqa_decode runs the wave kernel for groups of >= 4 q heads over <= 32 positions when nothing is asked
+    explicitly: its output is then bit-identical to bz_gqa_decode_wave's. Past 32 positions, or with an explicit split
+    count, it runs the split kernel (one split at these sizes)."""
+    rng = np.random.default_rng(77)
+    B, NH, NKV, D = 2, 8, 2, 128
+    for cap, routed in ((17, True), (32, True), (33, False), (64, False)):
+        q = bf16(rng.standard_normal((B, NH, D)), device)
+        k = bf16(rng.standard_normal((B, NKV, cap, D)), device)
+        v = bf16(rng.standard_normal((B, NKV, cap, D)), device)
+        lens = i32([cap, cap - 5], device)
+        auto = gqa_decode(q, k, v, lens, D ** -0.5)
+        wave = gqa_decode_wave(q, k, v, lens, D ** -0.5)
+        one = gqa_decode(q, k, v, lens, D ** -0.5, num_splits=1)
+        torch.cuda.synchronize()
+        check(auto[:, None], q[:, :, None], k, v, [cap, cap - 5], D ** -0.5, what=f"auto cap={cap}")
+        same = wave if routed else one
+        assert torch.equal(auto.view(torch.int16), same.view(torch.int16)), f"cap={cap} routed={routed}"
