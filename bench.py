@@ -43,6 +43,8 @@ def parse_args():
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--backbone-only", action="store_true",
                    help="only the 28-layer backbone decode step and its GEMVs (for profiling)")
+    p.add_argument("--depth-only", action="store_true",
+                   help="only the depth frames: config 5 (split and wave kernels) and the real depth shape")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--traffic-bytes", type=float, default=None,
                    help="HBM bytes per call (overrides the value read from profiles/)")
@@ -238,25 +240,11 @@ def time_backbone(pkg, dev, steps):
     return out
 
 
-def time_depth_frame(pkg, dev, steps, warmup, wave=False):
-    """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph; with
-    wave=True through bz_gqa_decode_wave (one wave per (row, q head), no split) instead of the split kernel."""
+def _time_frames(frame, nsteps, dev, steps, warmup):
+    """µs per frame of `frame` (nsteps launches), frames recorded back to back in one HIP graph."""
     import torch
-    from breeze_tts_2_flash_amd import workloads
 
-    w = workloads.make(5)
-    g = w.to(dev)
-    nsteps = g.q.shape[0]
-    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
     frames = max(1, steps // nsteps)
-
-    def frame():
-        for s in range(nsteps):
-            if wave:
-                pkg.gqa_decode_wave(g.q[s], g.k, g.v, g.seq_lens[s], g.scale, out=out)
-            else:
-                pkg.gqa_decode(g.q[s], g.k, g.v, g.seq_lens[s], g.scale, out=out, max_seq_len=nsteps)
-
     for _ in range(max(1, warmup // nsteps)):
         frame()
     torch.cuda.synchronize()
@@ -272,10 +260,56 @@ def time_depth_frame(pkg, dev, steps, warmup, wave=False):
     graph.replay()
     end.record(stream)
     torch.cuda.synchronize()
-    us_frame = start.elapsed_time(end) * 1000.0 / frames
+    return start.elapsed_time(end) * 1000.0 / frames
+
+
+def time_depth_frame(pkg, dev, steps, warmup, wave=False):
+    """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph; with
+    wave=True through bz_gqa_decode_wave (one wave per (row, q head), no split) instead of the split kernel."""
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    w = workloads.make(5)
+    g = w.to(dev)
+    nsteps = g.q.shape[0]
+    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
+
+    def frame():
+        for s in range(nsteps):
+            if wave:
+                pkg.gqa_decode_wave(g.q[s], g.k, g.v, g.seq_lens[s], g.scale, out=out)
+            else:
+                pkg.gqa_decode(g.q[s], g.k, g.v, g.seq_lens[s], g.scale, out=out, max_seq_len=nsteps)
+
+    us_frame = _time_frames(frame, nsteps, dev, steps, warmup)
     frame_bytes = sum(workloads.algorithmic_bytes([L, L], w.num_q_heads, w.num_kv_heads, w.head_dim)
                       for L in range(1, nsteps + 1))
     return us_frame, frame_bytes
+
+
+def time_real_depth_frame(pkg, dev, steps, warmup):
+    """The reference's depth-transformer attention shape (flash/depth.py:71, :130-131): B2 (the CFG pair), 8 q / 2 KV
+    heads of 128, a 17-slot cache, 16 steps attending over 2..17 positions (seed 6, N(0,1)), one launch per step in
+    one HIP graph. gqa_decode as called (it takes the wave kernel at this shape) and with the split kernel forced
+    (num_splits=1). Returns (µs per frame routed, µs per frame split kernel, algorithmic bytes per frame)."""
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    B, NH, NKV, D, cap, nsteps = 2, 8, 2, 128, 17, 16
+    gen = torch.Generator().manual_seed(6)
+    q = torch.randn(nsteps, B, NH, D, generator=gen).bfloat16().to(dev)
+    k = torch.randn(B, NKV, cap, D, generator=gen).bfloat16().to(dev)
+    v = torch.randn(B, NKV, cap, D, generator=gen).bfloat16().to(dev)
+    lens = [torch.full((B,), s + 2, dtype=torch.int32, device=dev) for s in range(nsteps)]
+    out = torch.empty(B, NH, D, dtype=torch.bfloat16, device=dev)
+    res = []
+    for splits in (0, 1):
+        def frame():
+            for s in range(nsteps):
+                pkg.gqa_decode(q[s], k, v, lens[s], D ** -0.5, out=out, num_splits=splits)
+        res.append(_time_frames(frame, nsteps, dev, steps, warmup))
+    frame_bytes = sum(workloads.algorithmic_bytes([L, L], NH, NKV, D) for L in range(2, nsteps + 2))
+    return res[0], res[1], frame_bytes
 
 
 def cpu_baseline(w, calls=200, warmup=20, kind="eager", budget_s=10.0):
@@ -374,6 +408,14 @@ def main():
         bb = time_backbone(pkg, dev, args.steps)
         print(json.dumps({"backbone": bb}), flush=True)
         return
+    if args.depth_only:
+        us_f, _ = time_depth_frame(pkg, dev, args.steps, args.warmup)
+        us_w, _ = time_depth_frame(pkg, dev, args.steps, args.warmup, wave=True)
+        us_r, us_rs, _ = time_real_depth_frame(pkg, dev, args.steps, args.warmup)
+        print(json.dumps({"config5_frame_us": round(us_f, 3), "config5_frame_wave_us": round(us_w, 3),
+                          "real_depth_frame_us": round(us_r, 3), "real_depth_frame_split_us": round(us_rs, 3)}),
+              flush=True)
+        return
     cfg = args.config
     w2 = workloads.make(cfg)
     splits2 = args.splits or pkg.default_splits(w2.batch, w2.num_kv_heads, w2.head_dim, w2.capacity, 0)
@@ -432,6 +474,12 @@ def main():
         extra["config5_depth_frame_wave"] = {"us_per_frame": round(us_w, 3), "us_per_call": round(us_w / 32, 3),
                                              "bytes_per_frame": fb, "GB/s": round(fb / us_w / 1e3, 1)}
         print(f"[bench] config 5 depth frame, one wave per (row, q head): {us_w:.3f} us/frame", file=sys.stderr, flush=True)
+        us_r, us_rs, rb = time_real_depth_frame(pkg, dev, args.steps, args.warmup)
+        extra["depth_real_frame"] = {"shape": "B2 8q/2kv D128, 16 steps over 2..17 positions",
+                                     "us_per_frame": round(us_r, 3), "us_per_call": round(us_r / 16, 3),
+                                     "split_kernel_us_per_frame": round(us_rs, 3), "bytes_per_frame": rb}
+        print(f"[bench] real depth shape frame: {us_r:.3f} us/frame ({us_rs:.3f} with the split kernel)",
+              file=sys.stderr, flush=True)
         bb = time_backbone(pkg, dev, args.steps)
         extra["backbone"] = bb
         for k, v in bb.items():
