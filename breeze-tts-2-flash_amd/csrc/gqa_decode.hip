@@ -80,13 +80,13 @@ int effective_len(int capacity, int max_seq_len) {
 
 // Split count: enough workgroups to give every CU one (cus / units splits), and no chunk longer than kMaxChunk
 // positions even in the longest row (a chunk streams through one workgroup two tiles at a time, so its latency grows
-// with its length), but no split shorter than min_chunk positions. A row whose whole K+V span fits kOneSplitBytes is
-// not split: the cross-workgroup merge of two or more splits (partials stored, counted, reloaded) costs about 2 us,
-// more than one workgroup takes to stream 64 KB (cold, B2 16/8: head_dim 128, 128 positions 4.45 against 5.42 us;
-// head_dim 64, 256 positions 4.47 against 5.17; at 128 KB one split is slower: 6.23 against 5.47).
+// with its length), but no split shorter than min_chunk positions. When the whole K+V span of the longest row fits
+// kOneSplitBytes there is one split (the kernels apply the same bound to each row's actual length): the
+// cross-workgroup merge of two or more splits costs about 2 us, more than one workgroup takes to stream 64 KB (cold,
+// B2 16/8: head_dim 128, 128 positions 4.45 against 5.42 us; head_dim 64, 256 positions 4.47 against 5.17; at 128 KB
+// one split is slower: 6.23 against 5.47).
 int default_splits_for(int units, int D, int len, int cus) {
   constexpr int kMaxChunk = 256;
-  constexpr int64_t kOneSplitBytes = 64 * 1024;
   if ((int64_t)len * 4 * D <= kOneSplitBytes) return 1;
   const int min_chunk = min_chunk_for(D);
   const int useful = len > 0 ? (len + min_chunk - 1) / min_chunk : 1;

@@ -11,8 +11,9 @@
 // Work decomposition (split-K over the KV length, "flash-decoding"):
 //   grid (splits, num_kv_heads, batch), NT = 256 threads (4 wave64) per workgroup.
 //   Each row's valid length is cut on the device into nact <= splits chunks of
-//   chunk = max(min_chunk, ceil(len / splits)) positions, so a fixed grid serves every length (HIP-graph safe) and
-//   the work follows the real length: workgroups past nact exit at once.
+//   chunk = max(min_chunk, ceil(len / splits)) positions (one chunk for a row whose K+V span is at most 64 KB), so a
+//   fixed grid serves every length (HIP-graph safe) and the work follows the real length: workgroups past nact exit
+//   at once.
 //   A workgroup streams its chunk in tiles of ROWS * PPT positions, two tiles in flight (ping-pong). A KV row of
 //   head_dim bf16 is read by LPR = head_dim / 8 consecutive lanes, 16 bytes each, so one wave64 load instruction
 //   covers 64 * 16 B of consecutive positions and every K/V byte is read once, by one lane, straight into VGPRs.
@@ -165,9 +166,19 @@ __device__ __forceinline__ void token_range(const Params& p, int b, int t, int& 
   end = max(start, end - (p.T - 1 - t));
 }
 
+// A row whose K+V span is at most kOneSplitBytes runs as one split whatever the grid: the cross-workgroup merge of two
+// or more splits (partials stored, counted, reloaded: about 2 us) costs more than one workgroup takes to stream that
+// much. The host's default split count applies the same bound to the capacity (or max_seq_len); here it applies to
+// each row's actual length, so a captured grid sized for the capacity serves the early, short steps too.
+constexpr int kOneSplitBytes = 64 * 1024;
+template <int D>
+constexpr int one_split_len() { return kOneSplitBytes / (4 * D); }
+
 // Positions per split and number of non-empty splits for a row of length len (>= 1 split even when empty, so
 // that someone writes the row's output).
+template <int D>
 __device__ __forceinline__ int split_chunk(int len, int splits, int min_chunk) {
+  if (len <= one_split_len<D>()) return len > min_chunk ? len : min_chunk;
   const int c = (len + splits - 1) / splits;
   return c > min_chunk ? c : min_chunk;
 }
@@ -432,7 +443,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   int start, end;
   token_range(p, b, tok, start, end);
   const int len = end - start;
-  const int chunk = split_chunk(len, p.splits, p.min_chunk);
+  const int chunk = split_chunk<D>(len, p.splits, p.min_chunk);
   const int nact = split_count(len, chunk);
   if (split >= nact) return;
   const int lo = start + split * chunk;
@@ -604,7 +615,7 @@ __global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
   int start, end;
   token_range(p, z / p.T, z % p.T, start, end);
   const int len = end - start;
-  const int nact = split_count(len, split_chunk(len, p.splits, p.min_chunk));
+  const int nact = split_count(len, split_chunk<D>(len, p.splits, p.min_chunk));
   if (nact == 1) return;  // the split kernel wrote the output
   merge_splits<D, G, kThreads>(p, z, h, nact);
 }

@@ -241,6 +241,20 @@ def test_one_split_up_to_64_kib(device, D, cap):
         assert np.array_equal(out, out1)
 
 
+def test_short_rows_run_as_one_split_in_a_wide_grid(device):
+    """A grid sized for the capacity (16 splits) runs a row whose K+V span is at most 64 KiB (128 positions at head_dim
+    128) as one chunk: bit-identical to the one-split launch. Longer rows in the same call are split and stay within
+    tolerance of the oracle."""
+    lens, starts = [100, 128, 129, 1500], [0, 0, 0, 37]
+    w, st = rand_case(131, 4, 16, 8, 128, 2048, lens, starts)
+    g = w.to(device)
+    wide = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=16)
+    one = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(wide[:2].view(torch.int16), one[:2].view(torch.int16))
+    assert_close(wide.float().cpu(), oracle(w, kv_start=st), "wide grid")
+
+
 # ---------------------------------------------------------------------------------------------- masks / compat
 
 @pytest.mark.parametrize("mdtype", [torch.bfloat16, torch.float32])
