@@ -1,4 +1,4 @@
-"""GPU parity of the one-wave-per-group attention (bz_gqa_decode_wave through gqa_decode_wave; its wave is the device
+"""GPU parity of the one-wave-per-(row, q head) attention (bz_gqa_decode_wave through gqa_decode_wave; its wave is the device
 function attend_wave of csrc/gqa_wave.cuh) against oracle.attention.decode_attention_tokens: head_dim 64 / 128 x
 group sizes 1 / 2 / 4 / 8 over edge lengths (empty, one position, tile and two-tile boundaries, several hundred
 positions) with non-zero starts; the depth transformer's shapes (the real 8 q / 2 KV heads at head_dim 128 and the
