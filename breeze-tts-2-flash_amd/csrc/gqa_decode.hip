@@ -180,6 +180,7 @@ bool wave_out_aligned(const bz_gqa_decode_args* a) {
 int launch_wave(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start) {
   const WaveFn fn = pick_wave(a->head_dim);
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
+  if ((int64_t)rows_of(a) * a->num_q_heads > INT32_MAX) return BZ_ERR_SHAPE;  // one workgroup per wave: grid.x
   const Params p = base_params(a, seq_lens, kv_start);
   const int waves = rows_of(a) * a->num_q_heads;
   hipLaunchKernelGGL(fn, dim3(waves), dim3(kWave), 0, stream, p, waves);
