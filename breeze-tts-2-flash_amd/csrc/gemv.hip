@@ -39,8 +39,14 @@ constexpr int kTileK = kChunk * kU;            // k elements per tile
 constexpr int kMaxLds = 64 * 1024;             // bytes of LDS for x
 // With x in registers every wave issues all its weight loads at once; spacing them by s_sleep(kIssueGap) (about
 // 64 * kIssueGap clocks) measured faster: q|k|v 5.06 against 5.19 us, gate/up 10.0 against 10.3-10.5. Gaps of 1, 3, 4
-// and 6 were tried; 2 was best or within noise of best.
+// and 6 were tried; 2 was best or within noise of best. It pays only when many workgroups contend for the memory
+// system; a small grid just waits longer for its last load (gate/up, M = 2, k = 2048: 12 workgroups 3.43 against
+// 2.89 us, 32 workgroups 4.05 against 3.92, 128 workgroups 4.25 against 4.43), so the host picks the paced variant
+// (GAP = kIssueGap) for grids of at least kPaceMinGrid workgroups. The gap is a template parameter, not a runtime
+// flag: a branch around each s_sleep split the loads over basic blocks, and the compiler's wait counts then went
+// pessimistic (the prologue waited for three more weight loads than it needs).
 constexpr int kIssueGap = 2;
+constexpr int kPaceMinGrid = 64;
 
 struct GemvParams {
   const uint16_t* x;
@@ -163,16 +169,18 @@ __device__ __forceinline__ void load_residual(const GemvParams& p, int row0, int
 
 // KC > 0: x held in registers, KC chunks per lane (k <= 512 KC <= 2 tiles): no LDS, and the RMSNorm's sum of squares
 // is reduced over the wave, so the prologue needs no barrier. KC == 0: x staged in LDS (any k).
-template <int M, int R, bool NORM, int EPI, int KC>
+template <int M, int R, bool NORM, int EPI, int KC, int GAP>
 __global__ void __launch_bounds__(gemv_threads<KC>()) gemv_kernel(const GemvParams p) {
+  static_assert(GAP == 0 || KC > 0, "issue pacing on the x-in-registers path only");
   constexpr int NT = gemv_threads<KC>(), NW = NT / kWave;
   constexpr int NR = EPI == BZ_GEMV_SILU_MUL ? 2 * R : R;  // weight rows per wave
   extern __shared__ __align__(16) uint16_t xs[];            // [M][kp] bf16
-  // With x in registers the wave index goes through a scalar register, so the weight resources are scalar and each
-  // load is one instruction. The LDS path leaves it in a VGPR, where the compiler issues every load from a
-  // one-iteration loop over the wave's distinct resources: measured faster there (down: 6.03 against 6.36 us with
-  // scalar resources, with or without pacing), for reasons not pinned down.
-  const int tid = threadIdx.x, lane = tid % kWave, wave = KC > 0 ? wave_uniform(tid / kWave) : tid / kWave;
+  // The paced variant takes the wave index through a scalar register, so the weight resources are scalar and each
+  // load is one instruction, spaced by s_sleep. The unpaced variants (x in LDS; small grids) leave it in a VGPR, where
+  // the compiler issues every load from a one-iteration loop over the wave's distinct resources. That measured faster
+  // than scalar resources without pacing, for reasons not pinned down (down: 6.03 against 6.36 us, paced or not;
+  // gate/up on 12 and 32 workgroups: 2.93 and 3.93 against 3.23 and 4.45 us).
+  const int tid = threadIdx.x, lane = tid % kWave, wave = GAP > 0 ? wave_uniform(tid / kWave) : tid / kWave;
   const int row0 = (blockIdx.x * NW + wave) * R;
 
   // this wave's weight rows (a row past the last output: an empty resource, whose loads read 0)
@@ -201,7 +209,7 @@ __global__ void __launch_bounds__(gemv_threads<KC>()) gemv_kernel(const GemvPara
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         t[r][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr[r], off, 0, kStream));
-        if constexpr (KC > 0) __builtin_amdgcn_s_sleep(kIssueGap);
+        if constexpr (GAP > 0) __builtin_amdgcn_s_sleep(GAP);
       }
     }
   };
@@ -383,33 +391,40 @@ __global__ void __launch_bounds__(kGemvThreads) rmsnorm_kernel(const uint16_t* x
 
 using GemvFn = void (*)(const GemvParams);
 
-template <int M, int R, int KC>
+template <int M, int R, int KC, int GAP>
 GemvFn pick_epi(int epi, bool norm) {
   if (epi == BZ_GEMV_PLAIN)
-    return norm ? gemv_kernel<M, R, true, BZ_GEMV_PLAIN, KC> : gemv_kernel<M, R, false, BZ_GEMV_PLAIN, KC>;
-  if (epi == BZ_GEMV_RESIDUAL) return norm ? nullptr : gemv_kernel<M, R, false, BZ_GEMV_RESIDUAL, KC>;
+    return norm ? gemv_kernel<M, R, true, BZ_GEMV_PLAIN, KC, GAP> : gemv_kernel<M, R, false, BZ_GEMV_PLAIN, KC, GAP>;
+  if (epi == BZ_GEMV_RESIDUAL) return norm ? nullptr : gemv_kernel<M, R, false, BZ_GEMV_RESIDUAL, KC, GAP>;
   if (epi == BZ_GEMV_SILU_MUL)
-    return norm ? gemv_kernel<M, R, true, BZ_GEMV_SILU_MUL, KC> : gemv_kernel<M, R, false, BZ_GEMV_SILU_MUL, KC>;
+    return norm ? gemv_kernel<M, R, true, BZ_GEMV_SILU_MUL, KC, GAP>
+                : gemv_kernel<M, R, false, BZ_GEMV_SILU_MUL, KC, GAP>;
   return nullptr;
 }
 
+// With x in LDS: R = 1, 2 or 4 rows per wave, no pacing. With x in registers: R = 2, paced or not.
 template <int M, int KC>
-GemvFn pick_r(int r, int epi, bool norm) {
-  switch (r) {
-    case 1: return pick_epi<M, 1, KC>(epi, norm);
-    case 2: return pick_epi<M, 2, KC>(epi, norm);
-    default: return pick_epi<M, 4, KC>(epi, norm);
+GemvFn pick_r(int r, int epi, bool norm, bool pace) {
+  if constexpr (KC > 0) {
+    if (r != 2) return nullptr;
+    return pace ? pick_epi<M, 2, KC, kIssueGap>(epi, norm) : pick_epi<M, 2, KC, 0>(epi, norm);
+  } else {
+    switch (r) {
+      case 1: return pick_epi<M, 1, KC, 0>(epi, norm);
+      case 2: return pick_epi<M, 2, KC, 0>(epi, norm);
+      default: return pick_epi<M, 4, KC, 0>(epi, norm);
+    }
   }
 }
 
 // x in registers for m * chunks <= 8 with m <= 2 (KC = 4: k <= 2048) or m <= 4 (KC = 2: k <= 1024); LDS otherwise.
 template <int M>
-GemvFn pick_kc(int kc, int r, int epi, bool norm) {
+GemvFn pick_kc(int kc, int r, int epi, bool norm, bool pace) {
   if constexpr (M <= 2) {
-    if (kc == 4) return pick_r<M, 4>(r, epi, norm);
+    if (kc == 4) return pick_r<M, 4>(r, epi, norm, pace);
   }
-  if (kc == 2) return pick_r<M, 2>(r, epi, norm);
-  return pick_r<M, 0>(r, epi, norm);
+  if (kc == 2) return pick_r<M, 2>(r, epi, norm, pace);
+  return pick_r<M, 0>(r, epi, norm, pace);
 }
 
 // Chunks of x per lane held in registers (0: x in LDS).
@@ -418,12 +433,12 @@ int kc_for(int m, int k) {
   return chunks <= 2 ? 2 : (chunks <= 4 && m <= 2 ? 4 : 0);
 }
 
-GemvFn pick_gemv(int m, int kc, int r, int epi, bool norm) {
+GemvFn pick_gemv(int m, int kc, int r, int epi, bool norm, bool pace) {
   switch (m) {
-    case 1: return pick_kc<1>(kc, r, epi, norm);
-    case 2: return pick_kc<2>(kc, r, epi, norm);
-    case 3: return pick_kc<3>(kc, r, epi, norm);
-    case 4: return pick_kc<4>(kc, r, epi, norm);
+    case 1: return pick_kc<1>(kc, r, epi, norm, pace);
+    case 2: return pick_kc<2>(kc, r, epi, norm, pace);
+    case 3: return pick_kc<3>(kc, r, epi, norm, pace);
+    case 4: return pick_kc<4>(kc, r, epi, norm, pace);
     default: return nullptr;
   }
 }
@@ -480,7 +495,10 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
 
   const int kc = kc_for(a->m, a->k);
   const int r = rows_per_wave(ntot, a->epilogue, kc);
-  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr);
+  const int threads = kc > 0 ? kGemvThreads : kGemvLdsThreads;
+  const int rows_per_block = threads / kWave * r;
+  const int grid = (ntot + rows_per_block - 1) / rows_per_block;
+  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr, grid >= kPaceMinGrid);
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   GemvParams p;
   p.x = static_cast<const uint16_t*>(a->x);
@@ -499,9 +517,6 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   p.ldy = a->y_stride;
   p.res = static_cast<const uint16_t*>(a->res);
   p.ldr = a->res_stride;
-  const int threads = kc > 0 ? kGemvThreads : kGemvLdsThreads;
-  const int rows_per_block = threads / kWave * r;
-  const int grid = (ntot + rows_per_block - 1) / rows_per_block;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), kc > 0 ? 0 : lds, stream, p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
