@@ -1,0 +1,87 @@
+"""Seeded random shapes through every attention entry against the oracle (oracle.attention.decode_attention_tokens).
+
+Each case draws batch 1..6, kv heads 1/2/4/8, group 1/2/4/8, head_dim 64/128, a capacity of 1..600 slots, per-row
+lengths 0..capacity and starts 0..length (empty and one-position rows included), 1 or 2 query tokens per row, a split
+count (0 = default, 1, 3, 8, 17), a merge mode and, in about a third of the cases, an additive mask (bf16 or fp32,
+values in [-2, 2] with excluded holes inside the range), with the K/V cache positions outside each row's range set to
+NaN. It runs bz_gqa_decode with the drawn options and, without a mask, bz_gqa_decode_wave. Tolerance
+|out - ref| <= 2e-3 + 1e-2 |ref| (the north star's), every output finite, rows with nothing to attend exactly 0.
+"""
+import numpy as np
+import pytest
+import torch
+
+from breeze_tts_2_flash_amd import gqa_decode, gqa_decode_wave
+from oracle.attention import decode_attention_tokens
+
+pytestmark = pytest.mark.gpu
+
+SEEDS = list(range(160))
+
+
+def draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 7))
+    NKV = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    D = int(rng.choice([64, 128]))
+    cap = int(rng.integers(1, 601))
+    T = int(rng.choice([1, 2]))
+    lens = rng.integers(0, cap + 1, size=B)
+    lens[rng.random(B) < 0.15] = 0
+    lens[rng.random(B) < 0.15] = 1
+    starts = np.array([int(rng.integers(0, L + 1)) if rng.random() < 0.5 else 0 for L in lens])
+    splits = int(rng.choice([0, 1, 3, 8, 17]))
+    combine = str(rng.choice(["auto", "last_block", "kernel"]))
+    q = rng.standard_normal((B, NKV * G, T, D)).astype(np.float32)
+    k = rng.standard_normal((B, NKV, cap, D)).astype(np.float32)
+    v = rng.standard_normal((B, NKV, cap, D)).astype(np.float32)
+    for b in range(B):  # NaN outside [start, end): never read, never leaks
+        k[b, :, :starts[b]] = v[b, :, :starts[b]] = np.nan
+        k[b, :, lens[b]:] = v[b, :, lens[b]:] = np.nan
+    mask = None
+    if rng.random() < 0.35:
+        mask = rng.uniform(-2.0, 2.0, size=(B, cap)).astype(np.float32)
+        mask[rng.random((B, cap)) < 0.1] = -np.inf if rng.random() < 0.5 else np.finfo(np.float32).min
+    mask_dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    return dict(B=B, NKV=NKV, G=G, D=D, cap=cap, T=T, lens=lens.astype(np.int32), starts=starts.astype(np.int32),
+                splits=splits, combine=combine, q=q, k=k, v=v, mask=mask, mask_dtype=mask_dtype)
+
+
+def bf16(a, device):
+    return torch.from_numpy(a).to(torch.bfloat16).to(device)
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_case(device, seed):
+    c = draw(seed)
+    what = (f"seed {seed}: B={c['B']} NKV={c['NKV']} G={c['G']} D={c['D']} cap={c['cap']} T={c['T']} "
+            f"lens={c['lens'].tolist()} starts={c['starts'].tolist()} splits={c['splits']} {c['combine']} "
+            f"mask={None if c['mask'] is None else c['mask_dtype']}")
+    print(what, flush=True)
+    q, k, v = (bf16(c[n], device) for n in ("q", "k", "v"))
+    lens = torch.from_numpy(c["lens"]).to(device)
+    starts = torch.from_numpy(c["starts"]).to(device)
+    scale = c["D"] ** -0.5
+    qb, kb, vb = (t.float().cpu().numpy() for t in (q, k, v))  # the bf16-rounded inputs the kernels see
+    mask = mb = None
+    if c["mask"] is not None:
+        mask = torch.from_numpy(c["mask"]).to(c["mask_dtype"]).to(device)[:, None, None, :]
+        mb = mask[:, 0, 0].float().cpu().numpy()
+    ref = decode_attention_tokens(qb, kb, vb, c["lens"], scale, kv_start=c["starts"], mask=mb)
+    outs = {"gqa_decode": gqa_decode(q, k, v, lens, scale, kv_start=starts, mask=mask, num_splits=c["splits"],
+                                     combine=c["combine"])}
+    if mask is None:
+        outs["gqa_decode_wave"] = gqa_decode_wave(q, k, v, lens, scale, kv_start=starts)
+    torch.cuda.synchronize()
+    for name, out in outs.items():
+        got = out.float().cpu().numpy().reshape(ref.shape)
+        assert np.isfinite(got).all(), f"{name} {what}: non-finite output"
+        excess = np.abs(got - ref) - (2e-3 + 1e-2 * np.abs(ref))
+        assert excess.max() <= 0, f"{name} {what}: excess {excess.max():.3e}"
+        for b in range(c["B"]):
+            for t in range(c["T"]):
+                s0, e0 = c["starts"][b], max(c["starts"][b], c["lens"][b] - (c["T"] - 1 - t))
+                live = e0 > s0 and (mb is None or (mb[b, s0:e0] > -1e30).any())
+                if not live:
+                    assert not got[b, t].any(), f"{name} {what}: row {b} token {t} attends nothing but is not zero"
