@@ -85,3 +85,32 @@ def test_random_case(device, seed):
                 live = e0 > s0 and (mb is None or (mb[b, s0:e0] > -1e30).any())
                 if not live:
                     assert not got[b, t].any(), f"{name} {what}: row {b} token {t} attends nothing but is not zero"
+
+
+FUSED_SEEDS = list(range(48))
+
+
+@pytest.mark.parametrize("seed", FUSED_SEEDS)
+def test_random_fused_step(device, seed):
+    """bz_gqa_decode_fused on seeded random shapes: batch 1..4, kv heads 1/2/4/8, group 1/2/4/8, head_dim 128, a
+    capacity of 1..600 slots, the new slot anywhere in the cache, each row attending up to and including it from a
+    random left-padding start (sometimes a shorter or longer row), random split count and merge mode. Checked with the
+    fused-step test's rules: output within tolerance, new k within one bf16 ulp, new v exact, other slots untouched."""
+    from tests.test_gpu_fused import check_against_oracle, make_step, run_fused
+
+    rng = np.random.default_rng(5000 + seed)
+    B = int(rng.integers(1, 5))
+    NKV = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    cap = int(rng.integers(1, 601))
+    pos = int(rng.integers(0, cap))
+    lens = [pos + 1 if rng.random() < 0.8 else int(rng.integers(0, cap + 1)) for _ in range(B)]
+    starts = [int(rng.integers(0, min(lens[b], pos + 1) + 1)) if rng.random() < 0.5 else 0 for b in range(B)]
+    splits = int(rng.choice([0, 1, 3, 8, 17]))
+    combine = str(rng.choice(["auto", "last_block", "kernel"]))
+    what = (f"fused seed {seed}: B={B} NKV={NKV} G={G} cap={cap} pos={pos} lens={lens} starts={starts} "
+            f"splits={splits} {combine}")
+    print(what, flush=True)
+    s = make_step(7000 + seed, B=B, NH=NKV * G, NKV=NKV, D=128, cap=cap, pos=pos)
+    out, kc, vc = run_fused(s, device, pos, lens, starts, num_splits=splits, combine=combine)
+    check_against_oracle(s, pos, lens, starts, out, kc, vc, what)
