@@ -13,6 +13,7 @@ import torch
 
 from breeze_tts_2_flash_amd import gqa_decode, gqa_decode_wave
 from oracle.attention import decode_attention_tokens
+from oracle.bf16 import f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -114,3 +115,62 @@ def test_random_fused_step(device, seed):
     s = make_step(7000 + seed, B=B, NH=NKV * G, NKV=NKV, D=128, cap=cap, pos=pos)
     out, kc, vc = run_fused(s, device, pos, lens, starts, num_splits=splits, combine=combine)
     check_against_oracle(s, pos, lens, starts, out, kc, vc, what)
+
+
+GEMV_SEEDS = list(range(64))
+
+
+@pytest.mark.parametrize("seed", GEMV_SEEDS)
+def test_random_gemv(device, seed):
+    """bz_gemv on seeded random shapes: M 1..4, K a multiple of 8 in 8..7168 (x in registers or in LDS), 1..3 segments
+    of 0..1500 rows (plain, optionally RMSNorm'ed), a residual epilogue, or gate/up + SiLU * up; x and y with padded row
+    strides. Grids from one workgroup to hundreds (the paced and unpaced variants). Tolerance and bit-exact fraction as
+    in the GEMV parity tests (the fraction only from 200 outputs up)."""
+    from breeze_tts_2_flash_amd import gemv_gateup, gemv_resid, gemv_seg
+    from oracle.gemv import gemv as gemv_ref
+    from tests.test_gpu_gemv import assert_gemv_close, dev_bf16, host_bits, rand_bits
+
+    rng = np.random.default_rng(9000 + seed)
+    M = int(rng.integers(1, 5))
+    K = 8 * int(rng.integers(1, 897))
+    kind = str(rng.choice(["seg", "resid", "gateup"]))
+    xpad = 8 * int(rng.integers(0, 3))
+    x_full = rand_bits(rng, M, K + xpad, scale=2.0)
+    x = dev_bf16(x_full, device)[:, :K]
+    xb = x_full[:, :K]
+    what = f"gemv seed {seed}: {kind} M={M} K={K} x_stride={K + xpad}"
+    if kind == "seg":
+        ns = [int(rng.integers(1, 1501))] + [int(rng.integers(0, 1501)) for _ in range(int(rng.integers(0, 3)))]
+        ws = [rand_bits(rng, n, K, scale=K ** -0.5) for n in ns]
+        norm = rng.random() < 0.5
+        nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)) if norm else None
+        N = sum(ns)
+        y = torch.empty(M, N + 8, dtype=torch.bfloat16, device=device)[:, :N]
+        wd = [dev_bf16(w, device) for w in ws] + [torch.empty(0, K, dtype=torch.bfloat16, device=device)] * (3 - len(ws))
+        gemv_seg(x, None if nw is None else dev_bf16(nw, device), 1e-6, wd[0], wd[1], wd[2], y)
+        ref = gemv_ref(xb, ws, nw, 1e-6)
+        frac = 0.98
+        what += f" segments={ns} norm={norm}"
+    elif kind == "resid":
+        N = int(rng.integers(1, 3001))
+        w = rand_bits(rng, N, K, scale=K ** -0.5)
+        res = rand_bits(rng, M, N, scale=3.0)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+        gemv_resid(x, dev_bf16(w, device), dev_bf16(res, device), y)
+        ref = gemv_ref(xb, [w], epilogue="residual", res_bits=res)
+        frac = 0.98
+        what += f" N={N}"
+    else:
+        N = int(rng.integers(1, 2001))
+        wg, wu = (rand_bits(rng, N, K, scale=K ** -0.5) for _ in range(2))
+        nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+        gemv_gateup(x, dev_bf16(nw, device), 1e-6, dev_bf16(wg, device), dev_bf16(wu, device), y)
+        ref = gemv_ref(xb, [wg, wu], nw, 1e-6, epilogue="silu_mul")
+        frac = 0.95
+        what += f" N={N}"
+    print(what, flush=True)
+    torch.cuda.synchronize()
+    if M * N < 200:  # too few outputs for a bit-exact fraction to mean anything: the tolerance alone
+        frac = 0.0
+    assert_gemv_close(host_bits(y), ref, what, frac)
