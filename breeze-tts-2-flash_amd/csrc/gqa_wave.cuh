@@ -46,7 +46,7 @@ __device__ __forceinline__ float rows_total(float x) {
 // Called by all 64 lanes of one wave (wave-uniform arguments).
 template <int D>
 __device__ void attend_wave(const WaveAttention& a) {
-  constexpr int G = 1;
+  constexpr int G = 1;  // one q head per wave: the group size of the shared tile code (consume_tile)
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   constexpr int LPR = D / 8, RPW = kWave / LPR, PPT = 2, TP = RPW * PPT;
   const int lane = __lane_id(), r = lane / LPR, c = lane % LPR;
