@@ -3,21 +3,23 @@
 The Python-side op shape the reference's call sites use (flash/csrc/bb_attn.cu:416-418: query, kc, vc, mask,
 scaling, ...), with seq_lens in the mask's place. Every call goes through the C ABI of libbz_gqa_decode.so
 (bz_gqa_decode, include/bz_gqa_decode.h); torch only provides device memory, the current stream and the device
-guard. Workspaces are cached per (device, sizes) like the reference's _workspace (flash/backbone.py:27-37), so a
-call allocates nothing after the first one and can be recorded into a HIP graph.
+guard. Workspaces are cached per (device, stream), as the reference caches its _workspace (flash/backbone.py:27-37),
+so a call allocates nothing once its stream's workspace is large enough and can be recorded into a HIP graph.
 
 Errors follow the reference (TORCH_CHECK -> RuntimeError, bb_attn.cu:377-388, :420-447).
 """
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 
 import torch
 
 from . import kernels
 
-_WS: dict = {}
+_WS: dict = {}            # (device, stream, groups) -> workspace
+_WS_RETIRED: list = []    # workspaces replaced by larger ones (kept: a captured graph may still use them)
 _WS_LOCK = threading.Lock()
 
 _COMBINE = {"auto": kernels.COMBINE_AUTO, "last_block": kernels.COMBINE_LAST_BLOCK, "kernel": kernels.COMBINE_KERNEL}
@@ -31,14 +33,22 @@ def _combine_code(combine) -> int:
     return _COMBINE[combine]
 
 
-def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, capacity: int,
-                    num_splits: int = 0, max_seq_len: int = 0) -> int:
-    """Scratch bytes bz_gqa_decode needs (bz_gqa_decode_workspace_size). num_splits=0 needs a current device."""
+@functools.lru_cache(maxsize=1024)
+def _workspace_bytes(device_index: int, batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                     capacity: int, num_splits: int, max_seq_len: int) -> int:
     n = ctypes.c_size_t(0)
     kernels.check(kernels.load().bz_gqa_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, capacity,
                                                                num_splits, max_seq_len, ctypes.byref(n)),
                   "bz_gqa_decode_workspace_size")
     return int(n.value)
+
+
+def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, capacity: int,
+                    num_splits: int = 0, max_seq_len: int = 0) -> int:
+    """Scratch bytes bz_gqa_decode needs (bz_gqa_decode_workspace_size). num_splits=0 needs a current device."""
+    # the default split count depends on the device's CU count: the cached size is per device
+    dev = torch.cuda.current_device() if num_splits == 0 and torch.cuda.is_available() else -1
+    return _workspace_bytes(dev, batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
 
 
 def default_splits(batch: int, num_kv_heads: int, head_dim: int, capacity: int, max_seq_len: int = 0) -> int:
@@ -51,21 +61,30 @@ def default_splits(batch: int, num_kv_heads: int, head_dim: int, capacity: int, 
 
 def get_workspace(device: torch.device, batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
                   capacity: int, num_splits: int = 0, max_seq_len: int = 0) -> torch.Tensor:
-    """Zero-initialised, cached scratch for these sizes on the device's current stream (the library keeps it
-    zero-ready between calls). One per stream: calls in flight on two streams must not share the split counters and
-    partials. The first call on a stream that is being captured into a HIP graph allocates it from the graph's pool
+    """The zero-filled scratch of the device's current stream for calls with batch * num_kv_heads groups (batch counts
+    rows times query tokens), at least as large as these sizes need.
+
+    A workspace begins with the arrival counters of those groups, which every call leaves at zero, and the rest is
+    written before it is read, so one workspace serves every call with the same groups, whatever its split count,
+    capacity or length. There is one per (device, stream, groups), because calls in flight on two streams must not
+    share counters and partials. A call that needs more room replaces it with a zeroed one at least twice as large;
+    the replaced one stays allocated (a captured graph may still use it), so the memory held stays under twice the
+    largest need. The first call on a stream that is being captured into a HIP graph allocates from the graph's pool
     (its zero fill is then replayed with the graph); an eager call on the capture stream beforehand avoids that."""
+    n = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
     stream = torch.cuda.current_stream(device).cuda_stream
-    key = (str(device), stream, batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
+    key = (str(device), stream, batch * num_kv_heads)
     with _WS_LOCK:
         ws = _WS.get(key)
-        if ws is None:
+        if ws is None or ws.numel() < n:
+            size = n if ws is None else max(n, 2 * ws.numel())
             with torch.cuda.device(device):
-                n = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
-                ws = torch.zeros(n, dtype=torch.uint8, device=device)
-            if ws.data_ptr() % 256:
+                new = torch.zeros(size, dtype=torch.uint8, device=device)
+            if new.data_ptr() % 256:
                 raise RuntimeError("workspace allocation is not 256-byte aligned")
-            _WS[key] = ws
+            if ws is not None:
+                _WS_RETIRED.append(ws)
+            _WS[key] = ws = new
         return ws
 
 

@@ -6,6 +6,8 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <mutex>
+#include <unordered_map>
 
 #include "bz_gqa_decode.h"
 #include "gqa_kernels.cuh"
@@ -100,17 +102,21 @@ int default_splits_for(int units, int D, int len, int cus) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Workspace: the arrival counters of every (row, kv head), one 256-byte line each, first, then the split partials:
+// (m, l) pairs and the G * D accumulators of each split. The counters are zero between calls (the merging workgroup
+// resets its counter) and sit at the same place whatever the split count or length, so one zero-filled workspace
+// serves every call with the same rows * kv heads that it is large enough for. The partials are written before they
+// are read in every call.
 struct WsLayout {
-  size_t acc, ml, counters, ranges, total;
+  size_t counters, ml, acc, total;
 };
 
-WsLayout ws_layout(int B, int NH, int NKV, int D, int splits) {
+WsLayout ws_layout(int rows, int NH, int NKV, int D, int splits) {
   WsLayout w;
-  w.acc = 0;
-  w.ml = align256(w.acc + (size_t)B * NH * splits * D * sizeof(float));
-  w.counters = align256(w.ml + (size_t)B * NH * splits * sizeof(float2));
-  w.ranges = align256(w.counters + (size_t)B * NKV * kCounterStride * sizeof(int));
-  w.total = align256(w.ranges + (size_t)2 * B * sizeof(int32_t));
+  w.counters = 0;
+  w.ml = (size_t)rows * NKV * kCounterStride * sizeof(int);
+  w.acc = align256(w.ml + (size_t)rows * NH * splits * sizeof(float2));
+  w.total = align256(w.acc + (size_t)rows * NH * splits * D * sizeof(float));
   return w;
 }
 
@@ -201,21 +207,46 @@ bool wave_route(const bz_gqa_decode_args* a, int mask_kind, const bz_gqa_decode_
          wave_out_aligned(a);
 }
 
-// Checks the workspace, picks the kernels and launches the split kernel (and, on request, the merge kernel),
-// or the wave kernel where wave_route says so.
-// f != nullptr selects the fused-prologue variant.
+// Workgroups of `fn` (NT threads) that fit on the device at once: the split kernel's merger waits for the other
+// splits of its group, so a one-launch merge is only used when every workgroup of the grid can be resident together
+// (larger grids take the merge kernel). Cached per kernel; the device's CU count is cached per device.
+std::mutex g_occ_mu;
+std::unordered_map<const void*, int> g_occ;
+
+int resident_workgroups(SplitFn fn, int nt, int cus, long long* out) {
+  int per_cu = 0;
+  {
+    std::lock_guard<std::mutex> lk(g_occ_mu);
+    auto it = g_occ.find(reinterpret_cast<const void*>(fn));
+    if (it != g_occ.end()) per_cu = it->second;
+  }
+  if (per_cu == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), nt, 0) != hipSuccess ||
+        per_cu <= 0)
+      return BZ_ERR_DEVICE;
+    std::lock_guard<std::mutex> lk(g_occ_mu);
+    g_occ[reinterpret_cast<const void*>(fn)] = per_cu;
+  }
+  *out = (long long)per_cu * cus;
+  return BZ_OK;
+}
+
+// Picks the kernels, checks the workspace and launches the split kernel (and, when asked or when the grid cannot be
+// resident at once, the merge kernel), or the wave kernel where wave_route says so (it needs no workspace).
+// seq_lens NULL: each row's range comes from the mask, scanned by the kernels themselves. f != nullptr selects the
+// fused-prologue variant.
 int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
            int mask_kind, const bz_gqa_decode_fused_args* f) {
   const int NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
   const int G = NH / NKV, R = rows_of(a);
+  if (a->combine < BZ_COMBINE_AUTO || a->combine > BZ_COMBINE_KERNEL) return BZ_ERR_COMBINE_MODE;
+  if (seq_lens != nullptr && wave_route(a, mask_kind, f)) return launch_wave(a, stream, seq_lens, kv_start);
   int splits = 0;
   int rc = resolve_splits(a, &splits);
   if (rc != BZ_OK) return rc;
-  if (a->combine < BZ_COMBINE_AUTO || a->combine > BZ_COMBINE_KERNEL) return BZ_ERR_COMBINE_MODE;
   const WsLayout ws = ws_layout(R, NH, NKV, D, splits);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
-  if (wave_route(a, mask_kind, f)) return launch_wave(a, stream, seq_lens, kv_start);
 
   const int min_chunk = min_chunk_for(D);
   const int len = effective_len(cap, a->max_seq_len);
@@ -226,16 +257,25 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt, f != nullptr);
   SplitFn comb_fn = pick_combine(D, G);
   if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
+  bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
+  if (!two_kernels && splits > 1) {
+    int cus = 0;
+    long long resident = 0;
+    rc = device_cus(&cus);
+    if (rc == BZ_OK) rc = resident_workgroups(split_fn, nt, cus, &resident);
+    if (rc != BZ_OK) return rc;
+    two_kernels = (long long)splits * NKV * R > resident;
+  }
 
   char* wsb = static_cast<char*>(a->workspace);
   Params p = base_params(a, seq_lens, kv_start);
   p.splits = splits;
   p.min_chunk = min_chunk;
-  const bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
+  p.mask_kind = mask_kind;
   p.combine_last = two_kernels ? 0 : 1;
-  p.part_acc = reinterpret_cast<float*>(wsb + ws.acc);
-  p.part_ml = reinterpret_cast<float2*>(wsb + ws.ml);
   p.counters = reinterpret_cast<int*>(wsb + ws.counters);
+  p.part_ml = reinterpret_cast<float2*>(wsb + ws.ml);
+  p.part_acc = reinterpret_cast<float*>(wsb + ws.acc);
   p.qkv = nullptr;
   p.qkv_sb = 0;
   p.qn_w = p.kn_w = p.cos = p.sin = nullptr;
@@ -287,29 +327,6 @@ int check_common(const bz_gqa_decode_args* a, bool need_q) {
   return BZ_OK;
 }
 
-// Launch the mask-interval kernel into the workspace's ranges segment; returns the [start, end) arrays.
-int mask_ranges(const bz_gqa_decode_args* a, hipStream_t stream, int32_t** start, int32_t** end) {
-  if (a->mask == nullptr) return BZ_ERR_NULL;
-  if (a->mask_dtype != BZ_MASK_BF16 && a->mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
-  int splits = 0;
-  int rc = resolve_splits(a, &splits);
-  if (rc != BZ_OK) return rc;
-  const WsLayout ws = ws_layout(rows_of(a), a->num_q_heads, a->num_kv_heads, a->head_dim, splits);
-  if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
-  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
-  int32_t* ranges = reinterpret_cast<int32_t*>(static_cast<char*>(a->workspace) + ws.ranges);
-  *start = ranges;
-  *end = ranges + a->batch;
-  if (a->mask_dtype == BZ_MASK_BF16)
-    hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_BF16>, dim3(a->batch), dim3(kThreads), 0, stream, a->mask,
-                       a->mask_stride_b, a->capacity, *start, *end);
-  else
-    hipLaunchKernelGGL(mask_range_kernel<BZ_MASK_F32>, dim3(a->batch), dim3(kThreads), 0, stream, a->mask,
-                       a->mask_stride_b, a->capacity, *start, *end);
-  if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
-  return BZ_OK;
-}
-
 int check_fused(const bz_gqa_decode_fused_args* f) {
   if (f == nullptr) return BZ_ERR_NULL;
   const bz_gqa_decode_args* a = &f->base;
@@ -345,10 +362,9 @@ __attribute__((visibility("default"))) int bz_gqa_decode(const bz_gqa_decode_arg
 __attribute__((visibility("default"))) int bz_gqa_decode_masked(const bz_gqa_decode_args* a, hipStream_t stream) {
   int rc = check_common(a, true);
   if (rc != BZ_OK) return rc;
-  int32_t *start = nullptr, *end = nullptr;
-  rc = mask_ranges(a, stream, &start, &end);
-  if (rc != BZ_OK) return rc;
-  return launch(a, stream, end, start, a->mask_dtype, nullptr);
+  if (a->mask == nullptr) return BZ_ERR_NULL;
+  if (a->mask_dtype != BZ_MASK_BF16 && a->mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  return launch(a, stream, nullptr, nullptr, a->mask_dtype, nullptr);
 }
 
 __attribute__((visibility("default"))) int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* f,
@@ -361,10 +377,9 @@ __attribute__((visibility("default"))) int bz_gqa_decode_fused(const bz_gqa_deco
     if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
     return launch(a, stream, a->seq_lens, a->kv_start, mk, f);
   }
-  int32_t *start = nullptr, *end = nullptr;
-  rc = mask_ranges(a, stream, &start, &end);
-  if (rc != BZ_OK) return rc;
-  return launch(a, stream, end, start, a->mask_dtype, f);
+  if (a->mask == nullptr) return BZ_ERR_NULL;
+  if (a->mask_dtype != BZ_MASK_BF16 && a->mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  return launch(a, stream, nullptr, nullptr, a->mask_dtype, f);
 }
 
 __attribute__((visibility("default"))) int bz_gqa_decode_wave(const bz_gqa_decode_args* a, hipStream_t stream) {

@@ -30,7 +30,7 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
@@ -109,12 +109,19 @@ def link_command(objdir: Path, out: Path) -> list[str]:
             *[str(objdir / (Path(src).stem + ".o")) for src in SOURCES]]
 
 
+STAMP_SOURCE = "bench_stamp.hip"
+STAMP_PATH = PKG_DIR / "libbz_bench_stamp.so"  # bench.py's GPU timestamp kernel; not part of the C ABI
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile libbz_gqa_decode.so for gfx950 in-tree (always recompiles). Returns its path."""
+    """Compile libbz_gqa_decode.so for gfx950 in-tree (always recompiles), and bench.py's timestamp helper
+    libbz_bench_stamp.so. Returns the path of libbz_gqa_decode.so."""
     tmp = LIB_PATH.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="bz_gqa_build_") as d:
         objdir = Path(d)
         cmds = compile_commands(objdir)
+        stamp_tmp = STAMP_PATH.with_suffix(".so.tmp")
+        cmds.append([hipcc(), *HIPCC_FLAGS, "-shared", str(CSRC / STAMP_SOURCE), "-o", str(stamp_tmp)])
 
         def run(cmd):
             if verbose:
@@ -126,6 +133,7 @@ def build(verbose: bool = False) -> Path:
         for cmd, res in zip(cmds, results):
             if res.returncode != 0:
                 raise RuntimeError(f"hipcc failed ({res.returncode}) on {cmd[-3]}:\n{res.stderr[-4000:]}")
+        os.replace(stamp_tmp, STAMP_PATH)
         res = run(link_command(objdir, tmp))
         if res.returncode != 0:
             raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{res.stderr[-4000:]}")

@@ -18,6 +18,11 @@
  *     into a HIP graph. The grid depends only on host arguments; lengths are read on the device.
  *   - Return value: BZ_OK (0) or a negative bz_status. Nothing is launched when a check fails. No call throws.
  *   - Calls are reentrant. Two calls that share one workspace must be ordered on one stream.
+ *   - A workspace starts with the split kernel's arrival counters, one per (row, kv head), which every call leaves
+ *     at zero; the rest is written before it is read. One zero-filled workspace therefore serves any sequence of
+ *     calls with the same batch * tokens_per_row * num_kv_heads (any split count, length, mask or entry point) that
+ *     it is large enough for. A call with another batch * tokens_per_row * num_kv_heads needs a workspace of its own
+ *     (or a fresh zero fill): its counters would lie on the previous layout's partials.
  */
 #ifndef BZ_GQA_DECODE_H
 #define BZ_GQA_DECODE_H
@@ -30,7 +35,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 6
+#define BZ_GQA_DECODE_ABI_VERSION 7
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -91,7 +96,8 @@ typedef struct bz_gqa_decode_args {
   int32_t max_seq_len;
   int32_t combine;            /* bz_combine_mode */
   /* caller-owned scratch of at least bz_gqa_decode_workspace_size() bytes, 256-byte aligned. It must be
-     zero-filled once before first use; the library leaves it ready for the next call. */
+     zero-filled once before first use; the library leaves it ready for the next call with the same
+     batch * tokens_per_row * num_kv_heads (see the conventions above). */
   void* workspace;
   size_t workspace_bytes;
   /* Query tokens per row, T (0 or 1: one). With T > 1 each row carries its last T positions as queries, causal

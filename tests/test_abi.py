@@ -150,11 +150,10 @@ def _ws(lib, *args):
 
 def test_workspace_size(lib):
     def layout(B, NH, NKV, D, S):
+        # the arrival counters (one 256-byte line per row and kv head), the (m, l) pairs, then the accumulators
         a = lambda x: (x + 255) // 256 * 256  # noqa: E731
-        acc = a(B * NH * S * D * 4)
-        ml = a(acc + B * NH * S * 8)
-        cnt = a(ml + B * NKV * 64 * 4)
-        return a(cnt + 2 * B * 4)
+        acc = a(B * NKV * 256 + B * NH * S * 8)
+        return a(acc + B * NH * S * D * 4)
     for B, NH, NKV, D, cap, S in [(2, 16, 8, 128, 2048, 32), (16, 16, 8, 128, 2048, 1), (2, 8, 2, 64, 17, 3),
                                   (1, 8, 8, 128, 4096, 256)]:
         rc, n = _ws(lib, B, NH, NKV, D, cap, S, 0)

@@ -1,0 +1,101 @@
+"""The workspace contract of bz_gqa_decode on the GPU: a workspace starts with one arrival counter per (row, kv head),
+which every call leaves at zero, and the rest (the split partials) is written before it is read. One zero-filled
+workspace therefore serves every call with the same rows * kv heads, whatever its split count, length, mask or
+entry point.
+
+Tolerance as in test_gpu_parity: |out - ref| <= 2e-3 + 1e-2 * |ref| against the float64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from breeze_tts_2_flash_amd import attention, gqa_decode, gqa_decode_fused, gqa_decode_masked, workspace_bytes
+from oracle.attention import interval_mask
+from tests.test_gpu_parity import assert_close, oracle, rand_case
+
+pytestmark = pytest.mark.gpu
+
+COUNTER_BYTES = 256  # one 256-byte line per (row, kv head) at the start of the workspace
+
+
+def _counters_clear(ws, groups, what):
+    torch.cuda.synchronize()
+    nz = int(torch.count_nonzero(ws[:groups * COUNTER_BYTES]))
+    assert nz == 0, f"{what}: {nz} counter bytes left nonzero"
+
+
+def test_alternating_split_counts_on_one_workspace(device):
+    """num_splits 32 and 8 (and the default) in turn on one workspace, with lengths that change every call: the
+    partial slots of one layout overlap the other's, and the counters stay in place and at zero."""
+    w, _ = rand_case(71, 2, 16, 8, 128, 2048, [2048, 2048])
+    g = w.to(device)
+    ws = torch.zeros(workspace_bytes(2, 16, 8, 128, 2048, 32), dtype=torch.uint8, device=device)
+    for i, (splits, L) in enumerate([(32, 2048), (8, 1500), (32, 700), (0, 1024), (8, 2048), (32, 65), (8, 333)]):
+        print(f"call {i}: splits={splits} L={L}", flush=True)
+        lens = torch.tensor([L, max(1, L - 17)], dtype=torch.int32)
+        out = gqa_decode(g.q, g.k, g.v, lens.to(device), g.scale, num_splits=splits, workspace=ws)
+        _counters_clear(ws, 2 * 8, f"call {i}")
+        assert_close(out.float().cpu(), oracle(w, lens=lens), f"call {i} splits={splits} L={L}")
+
+
+@pytest.mark.parametrize("combine", ["last_block", "kernel"])
+def test_entries_share_one_workspace(device, combine):
+    """Plain, masked and fused calls, one after another on one workspace (same rows * kv heads), each correct and
+    each leaving the counters at zero; the two-token causal step on a workspace of its own (twice the rows)."""
+    B, NH, NKV, D, cap = 2, 16, 8, 128, 2048
+    w, st = rand_case(73, B, NH, NKV, D, cap, [1800, 1700], [0, 9])
+    g = w.to(device)
+    ws = torch.zeros(workspace_bytes(B, NH, NKV, D, cap, 64), dtype=torch.uint8, device=device)
+    kw = dict(combine=combine, workspace=ws)
+    out = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=24, **kw)
+    _counters_clear(ws, B * NKV, "plain")
+    assert_close(out.float().cpu(), oracle(w, kv_start=st), "plain")
+
+    mask = interval_mask([0, 9], 1699, cap).to(device)
+    mask[0, 0, 0, 1700:1800] = 0.0  # row 0 attends [0, 1800)
+    out = gqa_decode_masked(g.q, g.k, g.v, mask, g.scale, num_splits=40, **kw)
+    _counters_clear(ws, B * NKV, "masked")
+    ref = oracle(w, kv_start=np.array([0, 9]), lens=torch.tensor([1800, 1700], dtype=torch.int32),
+                 mask=mask[:, 0, 0, :].float().cpu().numpy())
+    assert_close(out.float().cpu(), ref, "masked")
+
+    qkv = (torch.randn(B, (NH + 2 * NKV) * D, generator=torch.Generator().manual_seed(6)) * 2).bfloat16().to(device)
+    ones = torch.ones(D, dtype=torch.bfloat16, device=device)
+    cos = torch.ones(B, D, dtype=torch.bfloat16, device=device)
+    sin = torch.zeros(B, D, dtype=torch.bfloat16, device=device)
+    kc, vc = g.k.clone(), g.v.clone()
+    pos = torch.tensor([1799], dtype=torch.int64, device=device)
+    gqa_decode_fused(qkv, ones, ones, 1e-6, cos, sin, kc, vc, pos, g.scale, seq_lens=g.seq_lens, num_splits=16, **kw)
+    _counters_clear(ws, B * NKV, "fused")
+
+    out = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=24, **kw)
+    _counters_clear(ws, B * NKV, "plain again")
+    assert_close(out.float().cpu(), oracle(w, kv_start=st), "plain again")
+
+    ws2 = torch.zeros(workspace_bytes(2 * B, NH, NKV, D, cap, 24), dtype=torch.uint8, device=device)
+    q2 = torch.randn(B, NH, 2, D, generator=torch.Generator().manual_seed(5)).bfloat16()
+    out = gqa_decode(q2.to(device), g.k, g.v, g.seq_lens, g.scale, num_splits=24, combine=combine, workspace=ws2)
+    _counters_clear(ws2, 2 * B * NKV, "two tokens")
+    for t in range(2):
+        ref = oracle(w, q=q2[:, :, t], lens=w.seq_lens - (1 - t))
+        assert_close(out[:, t].float().cpu(), ref, f"two tokens, token {t}")
+
+
+def test_cached_workspace_stays_bounded(device):
+    """The DynamicCache route: the key length grows by one every step. The cached workspace of the stream grows
+    geometrically instead of one new workspace per length, and its counters stay at zero between calls."""
+    B, NH, NKV, D = 2, 16, 8, 128
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(B, NH, D, generator=g).bfloat16().to(device)
+    k = torch.randn(B, NKV, 1200, D, generator=g).bfloat16().to(device)
+    v = torch.randn(B, NKV, 1200, D, generator=g).bfloat16().to(device)
+    before = len(attention._WS) + len(attention._WS_RETIRED)
+    for L in range(64, 1200, 7):
+        kk, vv = k[:, :, :L].contiguous(), v[:, :, :L].contiguous()
+        lens = torch.full((B,), L, dtype=torch.int32, device=device)
+        gqa_decode(q, kk, vv, lens, D ** -0.5)
+    torch.cuda.synchronize()
+    grown = len(attention._WS) + len(attention._WS_RETIRED) - before
+    assert grown <= 8, f"{grown} workspaces allocated over 163 growing lengths"
+    ws = attention._WS[(str(device), torch.cuda.current_stream(device).cuda_stream, B * NKV)]
+    _counters_clear(ws, B * NKV, "cached workspace")
