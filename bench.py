@@ -6,10 +6,16 @@ A step is one decode-attention call (bz_gqa_decode through the C ABI) over one b
 head_dim 128, capacity 2048, seq_lens 1024); config 3 (KV 4096) is measured in the same run and reported under
 "extra", with the depth frame (config 5) and the ragged batch (config 4).
 
-Timing: W untimed eager calls, then K calls recorded into one HIP graph (torch.cuda.CUDAGraph), replayed once
-untimed and once timed between HIP events recorded on the stream the kernels run on. Cold cache: the K calls
-rotate over enough distinct K/V buffer sets that their valid bytes exceed 640 MB, more than the 256 MB MALL, so
-every call streams its K/V from HBM. value = algorithmic bytes per call / (timed µs per call), in GB/s.
+Timing: W untimed eager calls, then K calls recorded into one HIP graph (torch.cuda.CUDAGraph) between two GPU
+wall-clock stamps (a one-thread kernel captured before and after them, libbz_bench_stamp.so; two untimed calls at the
+head of the graph), replayed once untimed and once timed: the timed region holds exactly the K calls, without the
+graph replay's own fixed cost (about 8 us per replay).
+Cold: the calls rotate over enough distinct K/V buffer sets that their valid bytes exceed 16 GB (far more than the
+256 MB MALL and than the page translations the GPU holds), whatever K is, and a 1 GiB write (untimed) runs right
+before the timed replay, so every timed call streams its K/V from HBM, through cold translations, even when K is
+smaller than the set count. value = algorithmic bytes per call / (timed µs
+per call), in GB/s. The extras (configs 3 and 4, the fused step, the depth frames, the backbone step) use fixed call
+counts of their own, independent of K.
 
 The CPU baseline is the reference's PyTorch CPU attention path (repeat_kv + bf16 matmul + fp32 softmax + matmul,
 models/breeze.py:259-286, as restated in oracle/attention.py:eager_bf16) on the same workload, timed on this host.
@@ -80,10 +86,105 @@ def fused_inputs(w, dev):
     return qkv, qn, kn, cos, sin, cache_pos
 
 
+# Valid K/V bytes the cold calls rotate over. Far more than MI355X's 256 MB MALL, and more than the GPU's page
+# translations cover, so that every timed call is cold in both whatever the call count: with 640 MB of sets, 1000
+# calls ran config 3 4% faster than 20 calls (the 20 touched each set once after the flush; the 1000 reused warm
+# translations); with 16 GB the two agree within about 1%.
+ROTATE_BYTES = 16e9
+FLUSH_BYTES = 1 << 30       # untimed write right before each timed replay
+EXTRA_CALLS = 1000          # timed calls of each extra workload, whatever --steps is
+EXTRA_FRAMES = 200          # timed depth frames
+BACKBONE_REPS = 100         # timed backbone steps (and replays of each GEMV's 28-layer graph)
+
+_FLUSH = {}
+
+
+def flush_caches(dev):
+    """Write FLUSH_BYTES on the current stream: evicts the L2s and the MALL (more than four times their size), and
+    keeps the GPU busy for ~150 µs while the host goes on to submit what follows."""
+    import torch
+
+    buf = _FLUSH.get(dev)
+    if buf is None:
+        buf = _FLUSH[dev] = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+
+
+class GpuStamps:
+    """GPU wall-clock stamps taken by a one-thread kernel (libbz_bench_stamp.so) captured into a graph: two of them
+    around the timed calls measure those calls alone on the GPU. Events recorded outside a graph would also hold the
+    replay's own fixed cost (about 8 us per replay, 0.4 us per call at 20 calls), and ROCm allows no timing events
+    inside a captured graph."""
+
+    _lib = None
+
+    def __init__(self, dev, n=2):
+        import ctypes
+
+        import torch
+        from breeze_tts_2_flash_amd import kernels
+
+        if GpuStamps._lib is None:
+            lib = ctypes.CDLL(str(kernels.STAMP_PATH))
+            lib.bz_bench_stamp.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            lib.bz_bench_stamp_rate_khz.argtypes = [ctypes.POINTER(ctypes.c_int)]
+            GpuStamps._lib = lib
+        self.dev = dev
+        self.buf = torch.zeros(n, dtype=torch.int64, device=dev)
+        khz = ctypes.c_int(0)
+        if GpuStamps._lib.bz_bench_stamp_rate_khz(ctypes.byref(khz)) != 0 or khz.value <= 0:
+            raise RuntimeError("bz_bench_stamp_rate_khz failed")
+        self.us_per_tick = 1e3 / khz.value
+
+    def stamp(self, i):
+        import ctypes
+
+        import torch
+
+        stream = torch.cuda.current_stream(self.dev).cuda_stream
+        if GpuStamps._lib.bz_bench_stamp(ctypes.c_void_p(self.buf.data_ptr() + 8 * i), ctypes.c_void_p(stream)) != 0:
+            raise RuntimeError("bz_bench_stamp failed")
+
+    def us(self, i=0, j=1):
+        v = self.buf.cpu().tolist()
+        return (v[j] - v[i]) * self.us_per_tick
+
+
+def capture_timed(fn, dev, lead=None):
+    """A HIP graph of [lead()] stamp fn() stamp. Returns (graph, stamps)."""
+    import torch
+
+    st = GpuStamps(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        if lead is not None:
+            lead()
+        st.stamp(0)
+        fn()
+        st.stamp(1)
+    graph.replay()  # untimed: the first replay uploads the graph
+    torch.cuda.synchronize()
+    return graph, st
+
+
+def time_captured(timed, dev, flush=True):
+    """µs between the stamps of a capture_timed() graph in one replay, after a cache flush (cold data) or not."""
+    import torch
+
+    graph, st = timed
+    torch.cuda.synchronize()
+    if flush:
+        flush_caches(dev)
+    graph.replay()
+    torch.cuda.synchronize()
+    return st.us()
+
+
 def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=False):
-    """µs per call for workload w (one q per call) over `steps` calls; cold rotates distinct K/V buffer sets.
-    fused: each call is a fused decode step (bz_gqa_decode_fused) writing slot seq_len - 1 of its set (the same
-    values every time) and attending over it."""
+    """µs per call for workload w (one q per call) over `steps` calls; cold rotates distinct K/V buffer sets
+    (ROTATE_BYTES of valid K/V whatever `steps` is) and flushes the caches before the timed region. fused: each call
+    is a fused decode step (bz_gqa_decode_fused) writing slot seq_len - 1 of its set (the same values every time) and
+    attending over it. Returns (µs per call, algorithmic bytes per call, sets, rotated bytes)."""
     import torch
     from breeze_tts_2_flash_amd import workloads
 
@@ -91,8 +192,9 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=F
     lens = w.seq_lens.tolist()
     nb = workloads.fused_algorithmic_bytes if fused else workloads.algorithmic_bytes
     read_bytes = nb(lens, w.num_q_heads, w.num_kv_heads, w.head_dim)
-    nsets = max(16, math.ceil(640e6 / read_bytes)) if cold else 1
-    nsets = min(nsets, steps)
+    nsets = max(16, math.ceil(ROTATE_BYTES / read_bytes)) if cold else 1
+    lead = 2 if cold else 0  # untimed calls at the head of the graph, on sets of their own
+    nsets += lead
     ks = torch.empty((nsets,) + tuple(g.k.shape), dtype=g.k.dtype, device=dev)
     vs = torch.empty_like(ks)
     ks.copy_(g.k.expand_as(ks))
@@ -109,45 +211,48 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=F
         def run(k, v, o=None):
             return pkg.gqa_decode(g.q, k, v, g.seq_lens, g.scale, o, **kw)
 
-    def call(i):
-        run(ks[i % nsets], vs[i % nsets], out)
+    def call(i):  # timed call i uses set lead + i mod (nsets - lead); lead calls use sets 0 .. lead - 1
+        j = lead + i % (nsets - lead) if i >= 0 else lead + i
+        run(ks[j], vs[j], out)
 
     for i in range(warmup):
         call(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if eager:
-        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if cold:
+            flush_caches(dev)
         start.record(stream)
         for i in range(steps):
             call(i)
         end.record(stream)
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1000.0 / steps
     else:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        # GPU stamps around exactly the `steps` calls, after `lead` untimed calls on sets the timed calls do not use
+        def lead_calls():
+            for i in range(-lead, 0):
+                call(i)
+
+        def timed_calls():
             for i in range(steps):
                 call(i)
-        graph.replay()  # untimed: first replay uploads the graph
-        torch.cuda.synchronize()
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1000.0 / steps
+        us = time_captured(capture_timed(timed_calls, dev, lead=lead_calls), dev, flush=cold) / steps
     # the rotated sets hold identical data: the last call's output must equal a fresh call on set 0
     ref = run(ks[0], vs[0])
     torch.cuda.synchronize()
     if not torch.equal(out.view(torch.int16), ref.view(torch.int16)):
         raise RuntimeError("benchmark output differs from a direct call")
     del ks, vs
-    return us, read_bytes, nsets
+    torch.cuda.empty_cache()  # the next workload's sets need the memory (up to ~40 GB)
+    return us, read_bytes, nsets - lead, (nsets - lead) * read_bytes
 
 
 BACKBONE = dict(H=2048, nq=2048, nk=1024, inter=6144, layers=28, D=128, cap=2048, len=1024)
 
 
-def time_backbone(pkg, dev, steps):
+def time_backbone(pkg, dev, reps=BACKBONE_REPS):
     """The reference's backbone decode step at its serving shape (a Qwen3 of hidden 2048, 16 q / 8 KV heads of 128,
     intermediate 6144, 28 layers; the CFG pair, M = 2; KV 1024 of 2048 slots) on random-init weights: per layer
     gemv_seg (RMSNorm + q|k|v) -> gqa_decode_fused -> gemv_resid (o_proj) -> gemv_gateup -> gemv_resid (down), then
@@ -202,27 +307,18 @@ def time_backbone(pkg, dev, steps):
         pkg.rmsnorm(x, norm_w, eps, hidden)
 
     def graph_time(fn, reps):
+        """Median µs of `reps` replays of fn captured in one graph, each replay timed alone after a cache flush."""
         fn()
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            fn()
-        g.replay()
-        torch.cuda.synchronize()
-        stream = torch.cuda.current_stream(dev)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            g.replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) * 1000.0 / reps
+        timed = capture_timed(fn, dev)
+        return statistics.median(time_captured(timed, dev) for _ in range(reps))
 
     out = {}
     layer_bytes = 2 * ((nq + 2 * nk) * H + H * nq + 2 * I * H + H * I) + 2 * 2 * (nk // D) * c["len"] * D * M
-    us = graph_time(step, max(5, steps // 100))
+    us = graph_time(step, reps)
     out["backbone_step_28_layers"] = {"us": round(us, 1), "bytes": L * layer_bytes,
-                                      "GB/s": round(L * layer_bytes / us / 1e3, 1)}
+                                      "GB/s": round(L * layer_bytes / us / 1e3, 1),
+                                      "pct_of_peak_hbm": round(100.0 * L * layer_bytes / us / 1e3 / PEAK_HBM_GBS, 1)}
     # each GEMV alone, over the 28 layers' weights in turn (28 launches per replay)
     cases = {
         "gemv_qkv_norm": (lambda ly: pkg.gemv_seg(x0, ly["ln1"], eps, ly["wq"], ly["wk"], ly["wv"], qkv),
@@ -233,37 +329,29 @@ def time_backbone(pkg, dev, steps):
         "gemv_down_resid": (lambda ly: pkg.gemv_resid(act, ly["wd"], h1, hidden), 2 * H * I),
     }
     for name, (fn, wbytes) in cases.items():
-        us = graph_time(lambda: [fn(ly) for ly in layers], max(5, steps // 100)) / L
+        us = graph_time(lambda: [fn(ly) for ly in layers], reps) / L
         out[name] = {"us": round(us, 3), "weight_bytes": wbytes, "GB/s": round(wbytes / us / 1e3, 1),
                      "pct_of_peak_hbm": round(100.0 * wbytes / us / 1e3 / PEAK_HBM_GBS, 1)}
     del layers
     return out
 
 
-def _time_frames(frame, nsteps, dev, steps, warmup):
-    """µs per frame of `frame` (nsteps launches), frames recorded back to back in one HIP graph."""
+def _time_frames(frame, nsteps, dev, frames=EXTRA_FRAMES, warmup=2):
+    """µs per frame of `frame` (nsteps launches), `frames` frames recorded back to back in one HIP graph. The depth
+    transformer's K/V is written moments before it is read, so it is timed warm (no flush)."""
     import torch
 
-    frames = max(1, steps // nsteps)
-    for _ in range(max(1, warmup // nsteps)):
+    for _ in range(warmup):
         frame()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+
+    def all_frames():
         for _ in range(frames):
             frame()
-    graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    graph.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1000.0 / frames
+    return time_captured(capture_timed(all_frames, dev), dev, flush=False) / frames
 
 
-def time_depth_frame(pkg, dev, steps, warmup, wave=False):
+def time_depth_frame(pkg, dev, wave=False):
     """Config 5: µs per 32-step depth frame (one launch per step, seq_lens 1..32), recorded in one HIP graph; with
     wave=True through bz_gqa_decode_wave (one wave per (row, q head), no split) instead of the split kernel."""
     import torch
@@ -281,13 +369,13 @@ def time_depth_frame(pkg, dev, steps, warmup, wave=False):
             else:
                 pkg.gqa_decode(g.q[s], g.k, g.v, g.seq_lens[s], g.scale, out=out, max_seq_len=nsteps)
 
-    us_frame = _time_frames(frame, nsteps, dev, steps, warmup)
+    us_frame = _time_frames(frame, nsteps, dev)
     frame_bytes = sum(workloads.algorithmic_bytes([L, L], w.num_q_heads, w.num_kv_heads, w.head_dim)
                       for L in range(1, nsteps + 1))
     return us_frame, frame_bytes
 
 
-def time_real_depth_frame(pkg, dev, steps, warmup):
+def time_real_depth_frame(pkg, dev):
     """The reference's depth-transformer attention shape (flash/depth.py:71, :130-131): B2 (the CFG pair), 8 q / 2 KV
     heads of 128, a 17-slot cache, 16 steps attending over 2..17 positions (seed 6, N(0,1)), one launch per step in
     one HIP graph. gqa_decode as called (it takes the wave kernel at this shape) and with the split kernel forced
@@ -307,7 +395,7 @@ def time_real_depth_frame(pkg, dev, steps, warmup):
         def frame():
             for s in range(nsteps):
                 pkg.gqa_decode(q[s], k, v, lens[s], D ** -0.5, out=out, num_splits=splits)
-        res.append(_time_frames(frame, nsteps, dev, steps, warmup))
+        res.append(_time_frames(frame, nsteps, dev))
     frame_bytes = sum(workloads.algorithmic_bytes([L, L], NH, NKV, D) for L in range(2, nsteps + 2))
     return res[0], res[1], frame_bytes
 
@@ -325,7 +413,11 @@ def cpu_baseline(w, calls=200, warmup=20, kind="eager", budget_s=10.0):
     torch.set_num_threads(threads)
     if kind == "eager":
         q = w.q[:, :, None, :]
-        mask = interval_mask([0] * w.batch, int(w.seq_lens[0]) - 1, w.capacity)
+        # 0 on each row's [0, seq_len), finfo.min elsewhere: interval_mask's values with a per-row end (the ragged
+        # batch's rows differ in length; for equal lengths this is interval_mask([0] * B, seq_len - 1, capacity))
+        mask = interval_mask([0] * w.batch, w.capacity - 1, w.capacity)
+        pos = torch.arange(w.capacity)
+        mask[:, 0, 0, :].masked_fill_(pos[None, :] >= w.seq_lens.long()[:, None], torch.finfo(mask.dtype).min)
 
         def run():
             eager_bf16(q, w.k, w.v, mask, w.scale)
@@ -405,13 +497,13 @@ def main():
     pkg.load()
 
     if args.backbone_only:
-        bb = time_backbone(pkg, dev, args.steps)
+        bb = time_backbone(pkg, dev)
         print(json.dumps({"backbone": bb}), flush=True)
         return
     if args.depth_only:
-        us_f, _ = time_depth_frame(pkg, dev, args.steps, args.warmup)
-        us_w, _ = time_depth_frame(pkg, dev, args.steps, args.warmup, wave=True)
-        us_r, us_rs, _ = time_real_depth_frame(pkg, dev, args.steps, args.warmup)
+        us_f, _ = time_depth_frame(pkg, dev)
+        us_w, _ = time_depth_frame(pkg, dev, wave=True)
+        us_r, us_rs, _ = time_real_depth_frame(pkg, dev)
         print(json.dumps({"config5_frame_us": round(us_f, 3), "config5_frame_wave_us": round(us_w, 3),
                           "real_depth_frame_us": round(us_r, 3), "real_depth_frame_split_us": round(us_rs, 3)}),
               flush=True)
@@ -421,8 +513,8 @@ def main():
     splits2 = args.splits or pkg.default_splits(w2.batch, w2.num_kv_heads, w2.head_dim, w2.capacity, 0)
     print(f"[bench] config {cfg} cold, {args.steps} calls, splits={splits2}, combine={args.combine}", file=sys.stderr,
           flush=True)
-    us, nbytes, nsets = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
-                                   cold=True, fused=args.fused)
+    us, nbytes, nsets, rotated = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits,
+                                            args.eager, cold=True, fused=args.fused)
     gbs = nbytes / us / 1e3
     print(f"[bench] config {cfg} cold: {us:.3f} us/call, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
     line = {
@@ -433,8 +525,9 @@ def main():
                                                  if args.fused else ""),
                    "us_per_call": round(us, 3), "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                    "storage": "bf16", "splits": splits2, "combine": args.combine,
-                   "timing": "eager launches" if args.eager else "HIP graph replay, HIP events on the launch stream",
-                   "cache": f"cold: {nsets} rotating K/V sets", "algorithmic_bytes_per_call": nbytes},
+                   "timing": "eager launches" if args.eager else "HIP graph replay, GPU wall-clock stamps around the timed calls",
+                   "cache": {"mode": "cold", "sets": nsets, "rotated_bytes": rotated, "flush_bytes": FLUSH_BYTES},
+                   "algorithmic_bytes_per_call": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": args.traffic_bytes if args.traffic_bytes is not None else
@@ -442,45 +535,53 @@ def main():
     }
     extra = {}
     if not args.no_extra:
-        us_w, _, _ = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
-                                cold=False, fused=args.fused)
-        extra[f"config{cfg}_warm"] = {"us_per_call": round(us_w, 3), "GB/s": round(nbytes / us_w / 1e3, 1)}
+        us_w, _, _, _ = time_calls(pkg, w2, dev, EXTRA_CALLS, args.warmup, args.combine, args.splits, args.eager,
+                                   cold=False, fused=args.fused)
+        extra[f"config{cfg}_warm"] = {"us_per_call": round(us_w, 3), "GB/s": round(nbytes / us_w / 1e3, 1),
+                                      "calls": EXTRA_CALLS}
         print(f"[bench] config {cfg} warm: {us_w:.3f} us/call", file=sys.stderr, flush=True)
         for xc in (2, 3, 4):
             if xc == cfg:
                 continue
             w = workloads.make(xc)
-            us_c, nb, ns = time_calls(pkg, w, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
-                                      cold=True)
+            us_c, nb, ns, rot = time_calls(pkg, w, dev, EXTRA_CALLS, args.warmup, args.combine, args.splits,
+                                           args.eager, cold=True)
             extra[f"config{xc}_cold"] = {
                 "workload": workloads.NAMES[xc], "us_per_call": round(us_c, 3), "GB/s": round(nb / us_c / 1e3, 1),
-                "pct_of_peak_hbm": round(100.0 * nb / us_c / 1e3 / PEAK_HBM_GBS, 1), "bytes": nb, "sets": ns}
+                "pct_of_peak_hbm": round(100.0 * nb / us_c / 1e3 / PEAK_HBM_GBS, 1), "bytes": nb, "sets": ns,
+                "rotated_bytes": rot, "calls": EXTRA_CALLS}
             print(f"[bench] config {xc} cold: {us_c:.3f} us/call, {nb / us_c / 1e3:.1f} GB/s", file=sys.stderr,
                   flush=True)
             del w
         if not args.fused and w2.head_dim == 128 and len(set(w2.seq_lens.tolist())) == 1:
-            us_x, nbx, nsx = time_calls(pkg, w2, dev, args.steps, args.warmup, args.combine, args.splits, args.eager,
-                                        cold=True, fused=True)
+            us_x, nbx, nsx, rotx = time_calls(pkg, w2, dev, EXTRA_CALLS, args.warmup, args.combine, args.splits,
+                                              args.eager, cold=True, fused=True)
             extra[f"config{cfg}_fused_cold"] = {
                 "entry": "bz_gqa_decode_fused (q/k RMSNorm + RoPE + cache-slot write + attention)",
                 "us_per_call": round(us_x, 3), "GB/s": round(nbx / us_x / 1e3, 1),
-                "pct_of_peak_hbm": round(100.0 * nbx / us_x / 1e3 / PEAK_HBM_GBS, 1), "bytes": nbx, "sets": nsx}
+                "pct_of_peak_hbm": round(100.0 * nbx / us_x / 1e3 / PEAK_HBM_GBS, 1), "bytes": nbx, "sets": nsx,
+                "rotated_bytes": rotx, "calls": EXTRA_CALLS}
             print(f"[bench] config {cfg} fused cold: {us_x:.3f} us/call", file=sys.stderr, flush=True)
-        us_f, fb = time_depth_frame(pkg, dev, args.steps, args.warmup)
+        us_f, fb = time_depth_frame(pkg, dev)
         extra["config5_depth_frame"] = {"us_per_frame": round(us_f, 3), "us_per_call": round(us_f / 32, 3),
-                                        "bytes_per_frame": fb, "GB/s": round(fb / us_f / 1e3, 1)}
+                                        "bytes_per_frame": fb, "GB/s": round(fb / us_f / 1e3, 1),
+                                        "frames": EXTRA_FRAMES}
         print(f"[bench] config 5 depth frame: {us_f:.3f} us/frame", file=sys.stderr, flush=True)
-        us_w, _ = time_depth_frame(pkg, dev, args.steps, args.warmup, wave=True)
+        us_w, _ = time_depth_frame(pkg, dev, wave=True)
         extra["config5_depth_frame_wave"] = {"us_per_frame": round(us_w, 3), "us_per_call": round(us_w / 32, 3),
-                                             "bytes_per_frame": fb, "GB/s": round(fb / us_w / 1e3, 1)}
-        print(f"[bench] config 5 depth frame, one wave per (row, q head): {us_w:.3f} us/frame", file=sys.stderr, flush=True)
-        us_r, us_rs, rb = time_real_depth_frame(pkg, dev, args.steps, args.warmup)
+                                             "bytes_per_frame": fb, "GB/s": round(fb / us_w / 1e3, 1),
+                                             "frames": EXTRA_FRAMES}
+        print(f"[bench] config 5 depth frame, one wave per (row, q head): {us_w:.3f} us/frame", file=sys.stderr,
+              flush=True)
+        us_r, us_rs, rb = time_real_depth_frame(pkg, dev)
         extra["depth_real_frame"] = {"shape": "B2 8q/2kv D128, 16 steps over 2..17 positions",
                                      "us_per_frame": round(us_r, 3), "us_per_call": round(us_r / 16, 3),
-                                     "split_kernel_us_per_frame": round(us_rs, 3), "bytes_per_frame": rb}
+                                     "split_kernel_us_per_frame": round(us_rs, 3), "bytes_per_frame": rb,
+                                     "frames": EXTRA_FRAMES}
         print(f"[bench] real depth shape frame: {us_r:.3f} us/frame ({us_rs:.3f} with the split kernel)",
               file=sys.stderr, flush=True)
-        bb = time_backbone(pkg, dev, args.steps)
+        bb = time_backbone(pkg, dev)
+        bb["timing"] = f"median of {BACKBONE_REPS} graph replays, each after a {FLUSH_BYTES >> 20} MiB cache flush"
         extra["backbone"] = bb
         for k, v in bb.items():
             print(f"[bench] {k}: {v}", file=sys.stderr, flush=True)
@@ -493,12 +594,25 @@ def main():
                                           f"{w2.capacity}-slot cache with the interval mask, median of {n} calls "
                                           f"(10 s of CPU time) after 20 warmups"}
         print(f"[bench] cpu baseline: {us_cpu:.1f} us/call on {cores} threads", file=sys.stderr, flush=True)
-        # beside it: the reference's own CPU-runnable case (config 1) and the fp32 SDPA oracle on the headline inputs
+        # beside it: the reference's own CPU-runnable case (config 1), the eager chain on configs 3 and 4, and the
+        # fp32 SDPA oracle on the headline inputs
+        cx = {}
         us_c1, _, n1 = cpu_baseline(workloads.make(1), kind="eager", calls=100000, budget_s=3.0)
+        cx["config1_eager_us_per_call"], cx["config1_calls"] = round(us_c1, 1), n1
+        for xc in (2, 3, 4):
+            if xc == cfg:
+                continue
+            wx = workloads.make(xc)
+            us_x, _, nx = cpu_baseline(wx, kind="eager", calls=100000, warmup=5, budget_s=3.0)
+            bx = workloads.algorithmic_bytes(wx.seq_lens.tolist(), wx.num_q_heads, wx.num_kv_heads, wx.head_dim)
+            cx[f"config{xc}_eager_us_per_call"], cx[f"config{xc}_calls"] = round(us_x, 1), nx
+            cx[f"config{xc}_eager_GB/s"] = round(bx / us_x / 1e3, 3)
+            print(f"[bench] cpu config {xc} eager: {us_x:.1f} us/call", file=sys.stderr, flush=True)
+            del wx
         us_sd, _, nsd = cpu_baseline(w2, kind="sdpa", calls=100000, warmup=5, budget_s=3.0)
-        line["cpu_baseline"]["extra"] = {
-            "config1_eager_us_per_call": round(us_c1, 1), "config1_calls": n1,
-            f"config{cfg}_sdpa_fp32_us_per_call": round(us_sd, 1), f"config{cfg}_sdpa_calls": nsd}
+        cx[f"config{cfg}_sdpa_fp32_us_per_call"], cx[f"config{cfg}_sdpa_calls"] = round(us_sd, 1), nsd
+        cx["budget"] = "3 s of CPU time per extra case (median call after 5-20 warmups)"
+        line["cpu_baseline"]["extra"] = cx
         print(f"[bench] cpu config 1 eager: {us_c1:.1f} us/call; config {cfg} sdpa fp32: {us_sd:.1f} us/call",
               file=sys.stderr, flush=True)
     print(json.dumps(line), flush=True)
