@@ -101,6 +101,8 @@ def _collect(graph) -> dict:
         _need(shapes == ((nq, H), (nk, H), (nk, H), (H, nq), (I, H), (I, H), (H, I)), f"layer {i}: weight shapes")
     norm_w = _dev_bf16(model.norm.weight, "the final norm")
     dev = L0.wq.device
+    reason = kernels.device_unsupported(dev.index)
+    _need(reason is None, f"device {reason}")
     S = int(graph.max_seq_len)
     cache = graph.static_cache.layers
     _need(len(cache) == len(Ls), "the static cache and the model have different layer counts")
@@ -171,14 +173,25 @@ def fused_decode_step(graph) -> None:
     _logits_and_cfg(graph)
 
 
-def install(graph_cls) -> None:
-    """Replace graph_cls._decode_step (BackboneGraph's) with fused_decode_step; idempotent. The library is loaded
-    first, so a missing build fails here (flash/backbone.py:191-198)."""
+def install(graph_cls) -> bool:
+    """Replace graph_cls._decode_step (BackboneGraph's) with fused_decode_step; idempotent. Returns True when the step
+    is (already) replaced. A visible GPU other than gfx950 declines with the reason printed and the original step
+    kept (the reference's pre-flight, flash/support.py:67-84, flash/__init__.py:32-48); with no GPU visible the step is
+    patched and every CPU graph keeps its original step through prepare(). The library is loaded first, so a missing
+    or stale build fails here (flash/backbone.py:141-148)."""
+    import torch
+
+    if torch.cuda.is_available():
+        reason = kernels.device_unsupported()
+        if reason is not None:
+            print(f"[breeze_tts_2_flash_amd] backbone decode step not installed: {reason}", flush=True)
+            return False
     kernels.load()
     if "_decode_step" in ORIG:
-        return
+        return True
     ORIG["_decode_step"] = graph_cls._decode_step
     graph_cls._decode_step = fused_decode_step
+    return True
 
 
 def uninstall(graph_cls) -> None:

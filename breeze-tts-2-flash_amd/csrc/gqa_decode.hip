@@ -462,4 +462,9 @@ __attribute__((visibility("default"))) const char* bz_status_string(int status) 
 
 __attribute__((visibility("default"))) int bz_gqa_decode_abi_version(void) { return BZ_GQA_DECODE_ABI_VERSION; }
 
+#ifndef BZ_BUILD_ID
+#define BZ_BUILD_ID "unknown"
+#endif
+__attribute__((visibility("default"))) const char* bz_gqa_decode_build_id(void) { return BZ_BUILD_ID; }
+
 }  // extern "C"

@@ -28,6 +28,7 @@ import sys
 
 import torch
 
+from . import kernels
 from .attention import gqa_decode, gqa_decode_masked
 
 NAME = "mi355_decode"
@@ -75,6 +76,8 @@ def _hip_route(module, query, key, value, attention_mask, dropout) -> bool:
         return False
     if not (query.is_cuda and key.is_cuda and value.is_cuda):
         return False
+    if kernels.device_unsupported(query.device.index) is not None:
+        return False
     if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
         return False
     if dropout and module.training:
@@ -117,9 +120,19 @@ def mi355_decode_attention(module, query: torch.Tensor, key: torch.Tensor, value
 def install() -> str:
     """Register the attention function and the eager mask builder under NAME, and eager_attention under EAGER_NAME
     (idempotent). Returns NAME: pass it as attn_implementation (from_pretrained / from_config) or set it on a config,
-    as the reference does with its own implementation (flash/prefill_attn.py:41-46)."""
+    as the reference does with its own implementation (flash/prefill_attn.py:41-46). A visible GPU other than gfx950
+    declines: nothing is registered, the reason is printed and "eager" (transformers' own attention) is returned, as
+    the reference's pre-flight keeps the official path (flash/support.py:67-84). Calls on such a device that reach
+    mi355_decode_attention anyway go to eager attention."""
+    import torch
     from transformers import AttentionInterface
     from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, eager_mask
+
+    if torch.cuda.is_available():
+        reason = kernels.device_unsupported()
+        if reason is not None:
+            print(f"[breeze_tts_2_flash_amd] {NAME} attention not installed: {reason}", flush=True)
+            return "eager"
 
     AttentionInterface.register(NAME, mi355_decode_attention)
     ALL_MASK_ATTENTION_FUNCTIONS.register(NAME, eager_mask)

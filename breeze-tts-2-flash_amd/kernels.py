@@ -8,6 +8,7 @@ declares the C signatures for ctypes. There is no fallback: if the library is mi
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import os
 import shutil
 import subprocess
@@ -36,8 +37,21 @@ ABI_VERSION = 7
 EXPORTS = (
     "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_fused", "bz_gqa_decode_workspace_size",
     "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version", "bz_gemv", "bz_rmsnorm",
-    "bz_mask_interval", "bz_gqa_decode_wave",
+    "bz_mask_interval", "bz_gqa_decode_wave", "bz_gqa_decode_build_id",
 )
+
+
+def source_id() -> str:
+    """Hash of what the library is built from: the translation units, their headers, the C ABI headers and the hipcc
+    flags (sha256, first 16 hex digits). build() compiles it into the library (bz_gqa_decode_build_id) and load()
+    refuses a library whose id differs from the sources next to it, as the reference's loader rebuilds when a source
+    or a flag changes (flash/kernels.py:1-4, :64-79)."""
+    h = hashlib.sha256()
+    files = [CSRC / f for f in SOURCES + HEADERS] + sorted(INCLUDE.glob("*.h"))
+    for f in files:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
 
 MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
 COMBINE_AUTO, COMBINE_LAST_BLOCK, COMBINE_KERNEL = 0, 1, 2
@@ -100,8 +114,9 @@ def hipcc() -> str:
 
 def compile_commands(objdir: Path) -> list[list[str]]:
     """One hipcc -c command per translation unit (objects into objdir)."""
-    return [[hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o",
-             str(objdir / (Path(src).stem + ".o"))] for src in SOURCES]
+    sid = source_id()
+    return [[hipcc(), *HIPCC_FLAGS, f"-DBZ_BUILD_ID=\"{sid}\"", f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src),
+             "-o", str(objdir / (Path(src).stem + ".o"))] for src in SOURCES]
 
 
 def link_command(objdir: Path, out: Path) -> list[str]:
@@ -167,6 +182,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_mask_interval.restype = ctypes.c_int
     lib.bz_gqa_decode_wave.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p]
     lib.bz_gqa_decode_wave.restype = ctypes.c_int
+    lib.bz_gqa_decode_build_id.argtypes = []
+    lib.bz_gqa_decode_build_id.restype = ctypes.c_char_p
 
 
 def load() -> ctypes.CDLL:
@@ -179,12 +196,40 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; "
                                "g.build()'); there is no non-HIP fallback")
         lib = ctypes.CDLL(str(LIB_PATH))
+        if not hasattr(lib, "bz_gqa_decode_build_id"):
+            raise RuntimeError(f"{LIB_PATH} predates the build id: rebuild it")
         _declare(lib)
         ver = lib.bz_gqa_decode_abi_version()
         if ver != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}: rebuild it")
+        built, current = lib.bz_gqa_decode_build_id().decode(), source_id()
+        if built != current:
+            raise RuntimeError(f"{LIB_PATH} was built from other sources or flags (build id {built}, the sources next "
+                               f"to it hash to {current}): rebuild it (python -c 'import __graft_entry__ as g; "
+                               "g.build()')")
         _LIB = lib
         return lib
+
+
+_DEVICE_REASON: dict = {}
+
+
+def device_unsupported(index: int | None = None) -> str | None:
+    """None if GPU `index` (default: the current one) can run the kernels, else the reason: the library holds gfx950
+    code only. The pre-flight of the reference's installer (flash/support.py:67-84), which declines a GPU other than
+    the one its kernels were built for; cached per device."""
+    import torch
+
+    if not torch.cuda.is_available():
+        return "no GPU is visible"
+    idx = torch.cuda.current_device() if index is None else int(index)
+    reason = _DEVICE_REASON.get(idx, False)
+    if reason is False:
+        props = torch.cuda.get_device_properties(idx)
+        arch = getattr(props, "gcnArchName", "").split(":")[0]
+        reason = None if arch == ARCH else f"{props.name} ({arch or 'unknown architecture'}): the kernels are {ARCH} only"
+        _DEVICE_REASON[idx] = reason
+    return reason
 
 
 def status_string(code: int) -> str:

@@ -185,6 +185,11 @@ const char* bz_status_string(int status);
 /* BZ_GQA_DECODE_ABI_VERSION of the loaded library. */
 int bz_gqa_decode_abi_version(void);
 
+/* Identity of the sources and compiler flags the library was built from (a hex string; "unknown" when built without
+   one). The Python loader compares it with the sources next to the library and refuses a stale build, as the
+   reference's loader rebuilds its extension when a source or a flag changes (flash/kernels.py:1-4, :64-79). */
+const char* bz_gqa_decode_build_id(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -302,3 +302,14 @@ def test_missing_library_fails_loudly(K, tmp_path, monkeypatch):
     with pytest.raises(RuntimeError, match="missing"):
         backbone.install(Graph)
     assert Graph._decode_step is not backbone.fused_decode_step
+
+
+def test_stale_build_is_refused(K, monkeypatch):
+    """load() compares the library's build id with the hash of the sources next to it and refuses a library built from
+    other sources or flags (the reference's loader rebuilds then, flash/kernels.py:1-4, :64-79)."""
+    lib = K.load()
+    assert lib.bz_gqa_decode_build_id().decode() == K.source_id()
+    monkeypatch.setattr(K, "_LIB", None)
+    monkeypatch.setattr(K, "source_id", lambda: "0123456789abcdef")
+    with pytest.raises(RuntimeError, match="built from other sources"):
+        K.load()

@@ -131,3 +131,18 @@ def test_prepare_reasons():
     graph.batch_size = 5
     assert backbone.prepare(graph) is None
     assert graph._bz_unsupported.startswith("batch 5")
+
+
+def test_install_declines_other_gpus(monkeypatch, capsys):
+    """A visible GPU other than gfx950: install() returns False, prints the reason and keeps the original step."""
+    from breeze_tts_2_flash_amd import kernels
+
+    class _Declined(_PatchedGraph):
+        pass
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(kernels, "device_unsupported", lambda index=None: "Fake GPU (gfx000): the kernels are gfx950 only")
+    before = _Declined._decode_step
+    assert backbone.install(_Declined) is False
+    assert _Declined._decode_step is before
+    assert "not installed: Fake GPU" in capsys.readouterr().out

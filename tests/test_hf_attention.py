@@ -69,3 +69,16 @@ def test_eager_attention_matches_transformers_eager(q_len, G):
     want, want_w = qwen3.eager_attention_forward(mod, q, k, v, mask, scaling=D ** -0.5)
     got, got_w = hf_attention.eager_attention(mod, q, k, v, mask, scaling=D ** -0.5)
     assert torch.equal(got, want) and torch.equal(got_w, want_w)
+
+
+def test_install_declines_other_gpus(monkeypatch, capsys):
+    """A visible GPU other than gfx950: nothing is registered, "eager" is returned with the reason, and calls that
+    reach the function anyway take eager attention (the reference's pre-flight, flash/support.py:67-84)."""
+    from breeze_tts_2_flash_amd import kernels
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(kernels, "device_unsupported", lambda index=None: "Fake GPU (gfx000): the kernels are gfx950 only")
+    assert hf_attention.install() == "eager"
+    assert "not installed: Fake GPU" in capsys.readouterr().out
+    q = torch.zeros(1, 4, 1, 64, dtype=torch.bfloat16)
+    assert not hf_attention._hip_route(None, q, q, q, None, 0.0)
