@@ -231,12 +231,43 @@ int resident_workgroups(SplitFn fn, int nt, int cus, long long* out) {
   return BZ_OK;
 }
 
+// The static scratch of bz_gqa_decode_noalloc, for callers that cannot allocate (code under HIP graph capture,
+// torch.compile's CUDA-graph trees, serving loops that forbid allocation): device memory of the library itself, one
+// copy per device, held until the process ends. Its layout differs from a workspace's: the arrival counters of up to
+// kScratchGroups (row, kv head) groups sit at fixed places at its start whatever the call's sizes, so calls of any
+// sizes can follow one another on it (a workspace's counter region follows the call's own group count); the split
+// partials follow. The counters start at zero (a __device__ array is zero-initialised when the library is loaded)
+// and every call leaves them at zero (the merging workgroup resets its counter); the partials are written before
+// they are read. In host code `scratch` only names the symbol: its device address comes from hipGetSymbolAddress,
+// per device (scratch_address below).
+constexpr int kScratchGroups = 1024;
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices];
+
+// Device address of the current device's scratch, looked up once per device with that device current.
+int scratch_address(void** addr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return BZ_ERR_DEVICE;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return BZ_ERR_DEVICE;
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return BZ_OK;
+}
+
 // Picks the kernels, checks the workspace and launches the split kernel (and, when asked or when the grid cannot be
 // resident at once, the merge kernel), or the wave kernel where wave_route says so (it needs no workspace).
 // seq_lens NULL: each row's range comes from the mask, scanned by the kernels themselves. f != nullptr selects the
-// fused-prologue variant.
+// fused-prologue variant. scratch_base != nullptr: the static scratch (its address on the current device) instead of
+// a->workspace.
 int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start,
-           int mask_kind, const bz_gqa_decode_fused_args* f) {
+           int mask_kind, const bz_gqa_decode_fused_args* f, void* scratch_base = nullptr) {
   const int NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
   const int G = NH / NKV, R = rows_of(a);
   if (a->combine < BZ_COMBINE_AUTO || a->combine > BZ_COMBINE_KERNEL) return BZ_ERR_COMBINE_MODE;
@@ -244,9 +275,22 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   int splits = 0;
   int rc = resolve_splits(a, &splits);
   if (rc != BZ_OK) return rc;
-  const WsLayout ws = ws_layout(R, NH, NKV, D, splits);
-  if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
-  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
+  WsLayout ws;
+  char* wsb = nullptr;
+  if (scratch_base == nullptr) {
+    ws = ws_layout(R, NH, NKV, D, splits);
+    if (a->workspace == nullptr || a->workspace_bytes < ws.total) return BZ_ERR_WORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0) return BZ_ERR_ALIGNMENT;
+    wsb = static_cast<char*>(a->workspace);
+  } else {
+    if ((long long)R * NKV > kScratchGroups) return BZ_ERR_SCRATCH;
+    ws.counters = 0;
+    ws.ml = (size_t)kScratchGroups * kCounterStride * sizeof(int);
+    ws.acc = align256(ws.ml + (size_t)R * NH * splits * sizeof(float2));
+    ws.total = align256(ws.acc + (size_t)R * NH * splits * D * sizeof(float));
+    if (ws.total > kScratchBytes) return BZ_ERR_SCRATCH;
+    wsb = static_cast<char*>(scratch_base);
+  }
 
   const int min_chunk = min_chunk_for(D);
   const int len = effective_len(cap, a->max_seq_len);
@@ -267,7 +311,6 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
     two_kernels = (long long)splits * NKV * R > resident;
   }
 
-  char* wsb = static_cast<char*>(a->workspace);
   Params p = base_params(a, seq_lens, kv_start);
   p.splits = splits;
   p.min_chunk = min_chunk;
@@ -357,6 +400,24 @@ __attribute__((visibility("default"))) int bz_gqa_decode(const bz_gqa_decode_arg
   const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
   if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
   return launch(a, stream, a->seq_lens, a->kv_start, mk, nullptr);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_noalloc(const bz_gqa_decode_args* a, hipStream_t stream) {
+  int rc = check_common(a, true);
+  if (rc != BZ_OK) return rc;
+  void* sc = nullptr;
+  if (a->seq_lens != nullptr) {
+    const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
+    if (a->mask != nullptr && mk == BZ_MASK_NONE) return BZ_ERR_MASK_DTYPE;
+    rc = scratch_address(&sc);
+    if (rc != BZ_OK) return rc;
+    return launch(a, stream, a->seq_lens, a->kv_start, mk, nullptr, sc);
+  }
+  if (a->mask == nullptr) return BZ_ERR_NULL;
+  if (a->mask_dtype != BZ_MASK_BF16 && a->mask_dtype != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  rc = scratch_address(&sc);
+  if (rc != BZ_OK) return rc;
+  return launch(a, stream, nullptr, nullptr, a->mask_dtype, nullptr, sc);
 }
 
 __attribute__((visibility("default"))) int bz_gqa_decode_masked(const bz_gqa_decode_args* a, hipStream_t stream) {
@@ -456,6 +517,9 @@ __attribute__((visibility("default"))) const char* bz_status_string(int status) 
     case BZ_ERR_LAUNCH: return "kernel launch failed";
     case BZ_ERR_DEVICE: return "HIP device query failed";
     case BZ_ERR_COMBINE_MODE: return "combine must be BZ_COMBINE_AUTO, _LAST_BLOCK or _KERNEL";
+    case BZ_ERR_SCRATCH:
+      return "bz_gqa_decode_noalloc: more than 1024 (row, kv head) groups or 8 MiB of split partials for its static "
+             "scratch; use bz_gqa_decode with a workspace";
     default: return "unknown status";
   }
 }

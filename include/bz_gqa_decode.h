@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 7
+#define BZ_GQA_DECODE_ABI_VERSION 8
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -47,7 +47,8 @@ typedef enum bz_status {
   BZ_ERR_MASK_DTYPE = -6,     /* mask_dtype is not one of bz_mask_dtype */
   BZ_ERR_LAUNCH = -7,         /* hipLaunchKernelGGL / hipGetLastError reported an error */
   BZ_ERR_DEVICE = -8,         /* hipGetDevice / hipDeviceGetAttribute failed */
-  BZ_ERR_COMBINE_MODE = -9    /* combine is not one of bz_combine_mode */
+  BZ_ERR_COMBINE_MODE = -9,   /* combine is not one of bz_combine_mode */
+  BZ_ERR_SCRATCH = -10        /* bz_gqa_decode_noalloc: the sizes exceed its static scratch */
 } bz_status;
 
 typedef enum bz_mask_dtype {
@@ -115,6 +116,17 @@ typedef struct bz_gqa_decode_args {
    mask, groups of 4 or more q heads per kv head and at most 32 positions (max_seq_len, else capacity) it runs the
    kernel of bz_gqa_decode_wave (the depth transformer's shape); otherwise the split kernel. */
 int bz_gqa_decode(const bz_gqa_decode_args* args, hipStream_t stream);
+
+/* bz_gqa_decode without a workspace and without any allocation: args->workspace and args->workspace_bytes are ignored
+   and the split partials and arrival counters live in a static scratch of the library (8 MiB per device, held until
+   the process ends). No counterpart in the reference (which takes caller-owned workspaces); it is for callers that
+   cannot allocate: code under HIP graph capture (such as torch.compile's CUDA-graph trees) or serving loops that
+   forbid allocation. With args->seq_lens NULL the range of each row comes from args->mask, as in
+   bz_gqa_decode_masked. Limits: at most 1024 (row, kv head) groups (batch * tokens_per_row * num_kv_heads) and
+   8 MiB of split partials (batch * tokens_per_row * num_q_heads * splits * (head_dim + 2) * 4 bytes), else
+   BZ_ERR_SCRATCH. Every call on a device shares that device's scratch: calls that overlap in time on one device
+   (several streams, several host threads) race and must be ordered by the caller. */
+int bz_gqa_decode_noalloc(const bz_gqa_decode_args* args, hipStream_t stream);
 
 /* Bytes of workspace bz_gqa_decode needs for these sizes (num_splits as passed, 0 = default; with tokens_per_row
    T > 1 pass batch * T). Replaces the caller-side sizing of the reference's scores/cmax/part/counters buffers
