@@ -11,13 +11,14 @@ Public API:
   mask_interval(mask, capacity, ...)   the [kv_start, seq_lens) rows of an interval mask, once per decode step
   backbone.fused_decode_step(graph) / backbone.install(BackboneGraph)   the whole backbone decode step
   build() / load()   compile / open libbz_gqa_decode.so (C ABI: include/bz_gqa_decode.h, include/bz_gemv.h)
+  torch.ops.bz.*     the same entry points as torch operators (torch_ops.py), used while torch.compile traces
 """
 from .attention import (default_splits, get_workspace, gqa_decode, gqa_decode_fused, gqa_decode_masked,
                         gqa_decode_wave, mask_interval, workspace_bytes)
 from .compat import attn_decode, attn_decode_fused
 from .gemv import gemv_gateup, gemv_resid, gemv_seg, rmsnorm
 from .kernels import build, load
-from . import backbone, hf_attention
+from . import backbone, hf_attention, torch_ops
 
 __all__ = ["gqa_decode", "gqa_decode_masked", "gqa_decode_wave", "gqa_decode_fused", "attn_decode", "attn_decode_fused",
            "gemv_seg", "gemv_resid", "gemv_gateup", "rmsnorm", "mask_interval", "backbone",

@@ -161,6 +161,40 @@ def _int32_rows(t: torch.Tensor, B: int, name: str, device) -> torch.Tensor:
     return t
 
 
+def _run(a, dev, workspace, entry: str, static_scratch: bool = False) -> None:
+    """Launches bz_gqa_decode or bz_gqa_decode_masked (entry) on the device's current stream.
+
+    Without a workspace, a call made while that stream is being captured into a HIP graph, or with static_scratch
+    (the torch operators, which run inside compiled graphs), goes to bz_gqa_decode_noalloc: it uses the library's
+    static per-device scratch and allocates nothing. An allocation there would come from a graph's private pool,
+    which torch.compile's CUDA-graph trees require to hold only the graph's outputs (in their eager warm-up runs as
+    well as under capture). Calls on the scratch must not overlap in time on one device (graph replays or compiled
+    calls on several streams). Sizes beyond the scratch (BZ_ERR_SCRATCH) take the stream's cached workspace."""
+    lib = kernels.load()
+    with torch.cuda.device(dev):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        if workspace is None and (static_scratch or torch.cuda.is_current_stream_capturing()):
+            if entry == "bz_gqa_decode_masked":
+                a.seq_lens, a.kv_start = None, None  # the noalloc entry takes the range from the mask
+            rc = lib.bz_gqa_decode_noalloc(ctypes.byref(a), stream)
+            if rc != kernels.ERR_SCRATCH:
+                kernels.check(rc, "bz_gqa_decode_noalloc")
+                return
+        ws = workspace if workspace is not None else get_workspace(
+            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
+            a.num_splits, a.max_seq_len)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
+        kernels.check(getattr(lib, entry)(ctypes.byref(a), stream), entry)
+
+
+def _default_out(q: torch.Tensor) -> torch.Tensor:
+    """The output a call allocates when none is given: [B, NH, D] for one query token, [B, T, NH, D] for T > 1."""
+    B, NH = q.size(0), q.size(1)
+    if q.dim() == 4 and q.size(2) > 1:
+        return torch.empty(B, q.size(2), NH, q.size(3), dtype=torch.bfloat16, device=q.device)
+    return torch.empty(B, NH, q.size(-1), dtype=torch.bfloat16, device=q.device)
+
+
 def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
                scale: float, out: torch.Tensor | None = None, *, kv_start: torch.Tensor | None = None,
                mask: torch.Tensor | None = None, num_splits: int = 0, max_seq_len: int = 0,
@@ -173,7 +207,20 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
     out: [B, NH, D] (default for T = 1), [B, T, NH, D] (default for T > 1) or [B, NH, T, D] bf16. Returns out.
     With T > 1 query tokens, row b's tokens are its last T positions, causal among themselves: token t attends
     [kv_start[b], seq_lens[b] - (T - 1 - t)) (the depth transformer's first step, depth_frame.cu:221-227).
+    Under torch.compile the call is the registered operator torch.ops.bz.gqa_decode (one opaque graph node).
     """
+    if torch.compiler.is_compiling():
+        out = _default_out(q) if out is None else out
+        torch.ops.bz.gqa_decode(q, k_cache, v_cache, seq_lens, float(scale), out, kv_start, mask, int(num_splits),
+                                int(max_seq_len), _combine_code(combine), workspace)
+        return out
+    return _gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_splits, max_seq_len, combine,
+                       workspace)
+
+
+def _gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_splits, max_seq_len, combine,
+                workspace, static_scratch=False) -> torch.Tensor:
+    """gqa_decode's call through the C ABI (the body of the eager path and of torch.ops.bz.gqa_decode)."""
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
     a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
@@ -182,13 +229,7 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
         _check(mask.device == dev, "mask must be on the query's device")
         a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
         a.mask = mask.data_ptr()
-    with torch.cuda.device(dev):
-        ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
-            a.num_splits, a.max_seq_len)
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_gqa_decode(ctypes.byref(a), ctypes.c_void_p(stream)), "bz_gqa_decode")
+    _run(a, dev, workspace, "bz_gqa_decode", static_scratch)
     return out
 
 
@@ -198,7 +239,17 @@ def gqa_decode_wave(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     """gqa_decode computed by one wave per (row, token, q head) (bz_gqa_decode_wave: the device function attend_wave
     launched alone; no split, no workspace). Same shapes and ranges as gqa_decode (no mask); out must be 16-byte
     aligned with strides that are multiples of 8 elements. Faster than gqa_decode only on short rows already cached
-    (the real depth shape); it exists to test and time the device function a whole-step depth kernel would call."""
+    (the real depth shape); it exists to test and time the device function a whole-step depth kernel would call.
+    Under torch.compile the call is the registered operator torch.ops.bz.gqa_decode_wave."""
+    if torch.compiler.is_compiling():
+        out = _default_out(q) if out is None else out
+        torch.ops.bz.gqa_decode_wave(q, k_cache, v_cache, seq_lens, float(scale), out, kv_start)
+        return out
+    return _gqa_decode_wave(q, k_cache, v_cache, seq_lens, scale, out, kv_start)
+
+
+def _gqa_decode_wave(q, k_cache, v_cache, seq_lens, scale, out, kv_start) -> torch.Tensor:
+    """gqa_decode_wave's call through the C ABI."""
     a, out = _fill_args(q, k_cache, v_cache, scale, out, 0, 0, "auto")
     dev = q.device
     a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
@@ -214,20 +265,25 @@ def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
                       scale: float, out: torch.Tensor | None = None, *, num_splits: int = 0, max_seq_len: int = 0,
                       combine: str | int = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Interval-mask form (bz_gqa_decode_masked): each row's range is the first..last position with mask > -1e30,
-    derived on the device; the mask is added inside that range. Same shapes as gqa_decode."""
+    derived on the device; the mask is added inside that range. Same shapes as gqa_decode. Under torch.compile the
+    call is the registered operator torch.ops.bz.gqa_decode_masked."""
+    if torch.compiler.is_compiling():
+        out = _default_out(q) if out is None else out
+        torch.ops.bz.gqa_decode_masked(q, k_cache, v_cache, mask, float(scale), out, int(num_splits), int(max_seq_len),
+                                       _combine_code(combine), workspace)
+        return out
+    return _gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine, workspace)
+
+
+def _gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine,
+                       workspace, static_scratch=False) -> torch.Tensor:
+    """gqa_decode_masked's call through the C ABI."""
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
     _check(mask.device == dev, "mask must be on the query's device")
     a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
     a.mask = mask.data_ptr()
-    with torch.cuda.device(dev):
-        ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
-            a.num_splits, a.max_seq_len)
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_gqa_decode_masked(ctypes.byref(a), ctypes.c_void_p(stream)),
-                      "bz_gqa_decode_masked")
+    _run(a, dev, workspace, "bz_gqa_decode_masked", static_scratch)
     return out
 
 
@@ -267,8 +323,24 @@ def gqa_decode_fused(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
     qkv: [B, (NH + 2 NKV) * D] bf16 raw q | k | v projections; q_norm_weight, k_norm_weight: [D] bf16; cos, sin:
     [B, D] or [B, 1, D] bf16; cache_pos: int64 device tensor whose first element is the cache slot that receives the
     new k (q_norm/k_norm + RoPE applied) and v of every row. Then attends like gqa_decode over [kv_start, seq_lens),
-    or, with seq_lens=None, over the interval of `mask` (required then). head_dim 128.
+    or, with seq_lens=None, over the interval of `mask` (required then). head_dim 128. Under torch.compile the call
+    is the registered operator torch.ops.bz.gqa_decode_fused (it writes out and the two caches).
     """
+    if torch.compiler.is_compiling():
+        if out is None:
+            NKV, D = k_cache.size(1), k_cache.size(3)
+            out = torch.empty(qkv.size(0), qkv.size(1) // D - 2 * NKV, D, dtype=torch.bfloat16, device=qkv.device)
+        torch.ops.bz.gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, float(eps), cos, sin, k_cache, v_cache,
+                                      cache_pos, float(scale), out, seq_lens, kv_start, mask, int(num_splits),
+                                      int(max_seq_len), _combine_code(combine), workspace)
+        return out
+    return _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale,
+                             out, seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace)
+
+
+def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
+                      seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace) -> torch.Tensor:
+    """gqa_decode_fused's call through the C ABI."""
     _check(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.dtype == torch.bfloat16,
            "qkv must be a bf16 [B, (NH + 2 NKV) * D] tensor with a contiguous last dim")
     _check(k_cache.dim() == 4, "k_cache must be [B, NKV, capacity, D]")

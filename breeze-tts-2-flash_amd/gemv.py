@@ -61,7 +61,15 @@ def _args(x, y, epilogue) -> kernels.GemvArgs:
 def gemv_seg(x: torch.Tensor, nw: torch.Tensor | None, eps: float, W0: torch.Tensor, W1: torch.Tensor,
              W2: torch.Tensor, y: torch.Tensor, R: int = 2, U: int = 1, warps: int = 8) -> torch.Tensor:
     """y[:, 0:N0+N1+N2] = norm?(x) @ [W0; W1; W2]^T (bb_fused.cu:293-317). W1 / W2 may be empty tensors; nw None
-    skips the RMSNorm. Returns y."""
+    skips the RMSNorm. Returns y. Under torch.compile the call is the registered operator torch.ops.bz.gemv_seg."""
+    if torch.compiler.is_compiling():
+        torch.ops.bz.gemv_seg(x, nw, float(eps), W0, W1, W2, y)
+        return y
+    return _gemv_seg(x, nw, eps, W0, W1, W2, y)
+
+
+def _gemv_seg(x, nw, eps, W0, W1, W2, y) -> torch.Tensor:
+    """gemv_seg's call through the C ABI (the body of the eager path and of torch.ops.bz.gemv_seg)."""
     M, K = _x2d(x)
     N0 = _w(W0, K, "W0")
     N1 = _w(W1, K, "W1") if W1 is not None and W1.numel() else 0
@@ -82,7 +90,16 @@ def gemv_seg(x: torch.Tensor, nw: torch.Tensor | None, eps: float, W0: torch.Ten
 
 def gemv_resid(x: torch.Tensor, W: torch.Tensor, res: torch.Tensor, y: torch.Tensor, R: int = 2, U: int = 1,
                warps: int = 8) -> torch.Tensor:
-    """y = res + x @ W^T with the GEMV rounded to bf16 before the add, as eager (bb_fused.cu:319-335). Returns y."""
+    """y = res + x @ W^T with the GEMV rounded to bf16 before the add, as eager (bb_fused.cu:319-335). Returns y.
+    Under torch.compile the call is the registered operator torch.ops.bz.gemv_resid."""
+    if torch.compiler.is_compiling():
+        torch.ops.bz.gemv_resid(x, W, res, y)
+        return y
+    return _gemv_resid(x, W, res, y)
+
+
+def _gemv_resid(x, W, res, y) -> torch.Tensor:
+    """gemv_resid's call through the C ABI."""
     M, K = _x2d(x)
     N = _w(W, K, "W")
     _y(res, M, N, "res")
@@ -96,7 +113,16 @@ def gemv_resid(x: torch.Tensor, W: torch.Tensor, res: torch.Tensor, y: torch.Ten
 
 def gemv_gateup(x: torch.Tensor, nw: torch.Tensor, eps: float, Wg: torch.Tensor, Wu: torch.Tensor, y: torch.Tensor,
                 R: int = 1, U: int = 1, warps: int = 8) -> torch.Tensor:
-    """y = silu(norm(x) @ Wg^T) * (norm(x) @ Wu^T) at the eager rounding points (bb_fused.cu:337-356). Returns y."""
+    """y = silu(norm(x) @ Wg^T) * (norm(x) @ Wu^T) at the eager rounding points (bb_fused.cu:337-356). Returns y.
+    Under torch.compile the call is the registered operator torch.ops.bz.gemv_gateup."""
+    if torch.compiler.is_compiling():
+        torch.ops.bz.gemv_gateup(x, nw, float(eps), Wg, Wu, y)
+        return y
+    return _gemv_gateup(x, nw, eps, Wg, Wu, y)
+
+
+def _gemv_gateup(x, nw, eps, Wg, Wu, y) -> torch.Tensor:
+    """gemv_gateup's call through the C ABI."""
     M, K = _x2d(x)
     N = _w(Wg, K, "Wg")
     _check(_w(Wu, K, "Wu") == N, "Wg and Wu must have the same number of rows")
@@ -111,7 +137,16 @@ def gemv_gateup(x: torch.Tensor, nw: torch.Tensor, eps: float, Wg: torch.Tensor,
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor) -> torch.Tensor:
-    """y = Qwen3RMSNorm(x) row by row (bb_fused.cu:358-368). Returns y."""
+    """y = Qwen3RMSNorm(x) row by row (bb_fused.cu:358-368). Returns y. Under torch.compile the call is the registered
+    operator torch.ops.bz.rmsnorm."""
+    if torch.compiler.is_compiling():
+        torch.ops.bz.rmsnorm(x, w, float(eps), y)
+        return y
+    return _rmsnorm(x, w, eps, y)
+
+
+def _rmsnorm(x, w, eps, y) -> torch.Tensor:
+    """rmsnorm's call through the C ABI."""
     _check(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
            "x must be a bf16 [M, K] device tensor with a contiguous last dim")
     M, K = x.shape

@@ -55,6 +55,7 @@ def source_id() -> str:
 
 MASK_NONE, MASK_BF16, MASK_F32 = 0, 1, 2
 COMBINE_AUTO, COMBINE_LAST_BLOCK, COMBINE_KERNEL = 0, 1, 2
+ERR_SCRATCH = -10  # BZ_ERR_SCRATCH: the sizes exceed bz_gqa_decode_noalloc's static scratch
 
 
 class GqaDecodeArgs(ctypes.Structure):

@@ -1,7 +1,8 @@
 """GPU: the whole backbone decode step through breeze_tts_2_flash_amd.backbone (the reference's fused step,
 flash/backbone.py:112-136, in place of BackboneGraph._decode_step) on the stand-in BackboneGraph of
 tests/mini_backbone_graph.py: a random-init bf16 Qwen3 backbone (head_dim 128, 2 layers), a 256-slot static cache
-holding 100 prefilled positions, left padding, codebook embeddings, the fp32 lm_head and CFG.
+holding 100 prefilled positions (and a 1024-slot cache holding 600, whose rows span many splits), left padding,
+codebook embeddings, the fp32 lm_head and CFG.
 
 - Against the CPU oracle of the step (oracle_step: oracle.gemv.decoder_layer per layer + the final RMSNorm):
   |hidden - ref| <= 2^-5 |ref| + 1e-2 rms(ref) (the attention output's 2e-3 + 1e-2 |ref| carried through o_proj and
@@ -46,10 +47,12 @@ def _restore(graph, snap):
         c.values.copy_(v)
 
 
-@pytest.mark.parametrize("batch,pads", [(2, [0, 7]), (1, [3]), (4, [0, 5, 0, 12])])
-def test_step_matches_oracle_and_eager(device, eager_name, batch, pads):
-    graph = build_graph(device, batch=batch, prefill=100, attn_implementation=eager_name, seed=batch)
-    pos = 100
+# the last case spreads each row over many splits: a 1024-slot cache, 600 filled, left padding up to 250
+@pytest.mark.parametrize("batch,pads,cap,pos", [(2, [0, 7], 256, 100), (1, [3], 256, 100),
+                                               (4, [0, 5, 0, 12], 256, 100), (2, [250, 0], 1024, 600)])
+def test_step_matches_oracle_and_eager(device, eager_name, batch, pads, cap, pos):
+    graph = build_graph(device, batch=batch, max_seq_len=cap, prefill=pos, attn_implementation=eager_name,
+                        seed=batch)
     print(f"backbone step: batch {batch}, pads {pads}, cache_pos {pos}", flush=True)
     ids = _ids(graph, 5)
     graph.set_step(ids, pads, pos)
@@ -89,10 +92,10 @@ class _CapturedGraph(MiniBackboneGraph):
     """A subclass, so that install() patches this class only."""
 
 
-def test_installed_step_in_a_hip_graph(device, eager_name):
-    graph = build_graph(device, batch=2, prefill=100, attn_implementation=eager_name, seed=11)
+@pytest.mark.parametrize("pads,cap,pos0", [([0, 7], 256, 100), ([250, 0], 1024, 600)])
+def test_installed_step_in_a_hip_graph(device, eager_name, pads, cap, pos0):
+    graph = build_graph(device, batch=2, max_seq_len=cap, prefill=pos0, attn_implementation=eager_name, seed=11)
     graph.__class__ = _CapturedGraph
-    pads, pos0 = [0, 7], 100
     backbone.install(_CapturedGraph)
     try:
         graph.set_step(_ids(graph, 1), pads, pos0)

@@ -99,3 +99,37 @@ def test_cached_workspace_stays_bounded(device):
     assert grown <= 8, f"{grown} workspaces allocated over 163 growing lengths"
     ws = attention._WS[(str(device), torch.cuda.current_stream(device).cuda_stream, B * NKV)]
     _counters_clear(ws, B * NKV, "cached workspace")
+
+
+def test_capture_without_workspace_allocates_nothing(device):
+    """A call recorded into a HIP graph without a workspace runs on the library's static scratch
+    (bz_gqa_decode_noalloc): the capture adds no cached workspace, and every replay, with eager calls of other sizes
+    in between, equals the eager result bit for bit; the masked form likewise (its range comes from the mask)."""
+    w, st = rand_case(79, 2, 16, 8, 128, 1024, [1000, 640], [0, 17])
+    g = w.to(device)
+    starts = st.to(device)
+    mask = interval_mask([0, 17], 639, 1024).to(device)
+    mask[0, 0, 0, 640:1000] = 0.0
+    ref = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=starts, num_splits=16)
+    ref_m = gqa_decode_masked(g.q, g.k, g.v, mask, g.scale, num_splits=16)
+    out = torch.empty_like(ref)
+    out_m = torch.empty_like(ref_m)
+    keys = set(attention._WS)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, out, kv_start=starts, num_splits=16)
+            gqa_decode_masked(g.q, g.k, g.v, mask, g.scale, out_m, num_splits=16)
+    assert set(attention._WS) == keys, "the capture allocated a workspace"
+    small = gqa_decode(g.q[:1], g.k[:1], g.v[:1], g.seq_lens[:1], g.scale, num_splits=8)
+    for i in range(3):
+        out.zero_()
+        out_m.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+        assert torch.equal(out_m.view(torch.int16), ref_m.view(torch.int16)), f"replay {i} (masked)"
+        again = gqa_decode(g.q[:1], g.k[:1], g.v[:1], g.seq_lens[:1], g.scale, num_splits=8)
+        assert torch.equal(again.view(torch.int16), small.view(torch.int16)), f"eager call after replay {i}"
