@@ -400,6 +400,51 @@ def time_real_depth_frame(pkg, dev):
     return res[0], res[1], frame_bytes
 
 
+HOST_CALLS = 500            # calls per host-overhead sample (5 samples, median)
+
+
+def host_overhead(pkg, dev):
+    """Eager host cost per call of the Python entry points on config 1's inputs (B2, 256 positions: every kernel
+    takes a few microseconds of GPU time, so the host is the bound): HOST_CALLS back-to-back calls without a
+    synchronisation, wall time / calls, median of 5 samples after 50 warmups. 'direct' is the package function (the
+    eager path: argument checks, ctypes structure, C ABI); 'torch_op' the registered operator torch.ops.bz.* called
+    eagerly (what a compiled graph calls, plus the dispatcher)."""
+    import torch
+    from breeze_tts_2_flash_amd import gemv_resid, gqa_decode, gqa_decode_fused, workloads
+
+    w = workloads.make(1).to(dev)
+    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
+    qkv, qn, kn, cos, sin, pos = fused_inputs(workloads.make(1), dev)
+    kc, vc = w.k.clone(), w.v.clone()
+    x = torch.randn(2, 1024, device=dev).bfloat16()
+    W = (torch.randn(1024, 1024, device=dev) * 0.03).bfloat16()
+    res = torch.randn(2, 1024, device=dev).bfloat16()
+    y = torch.empty_like(res)
+    cases = {
+        "gqa_decode_direct": lambda: gqa_decode(w.q, w.k, w.v, w.seq_lens, w.scale, out),
+        "gqa_decode_torch_op": lambda: torch.ops.bz.gqa_decode(w.q, w.k, w.v, w.seq_lens, float(w.scale), out, None,
+                                                               None, 0, 0, 0, None),
+        "gqa_decode_fused_direct": lambda: gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc, vc, pos, w.scale, out,
+                                                            seq_lens=w.seq_lens),
+        "gemv_resid_direct": lambda: gemv_resid(x, W, res, y),
+        "gemv_resid_torch_op": lambda: torch.ops.bz.gemv_resid(x, W, res, y),
+    }
+    got = {}
+    for name, fn in cases.items():
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            for _ in range(HOST_CALLS):
+                fn()
+            samples.append((time.perf_counter() - t0) * 1e6 / HOST_CALLS)
+            torch.cuda.synchronize()
+        got[name] = round(statistics.median(samples), 2)
+    return got
+
+
 def cpu_baseline(w, calls=200, warmup=20, kind="eager", budget_s=10.0):
     """Median µs per call on the host of the reference's CPU attention for workload w. kind "eager": the eager chain
     (repeat_kv + bf16 matmul + fp32 softmax + matmul, oracle/attention.py:eager_bf16) over the StaticCache capacity with
@@ -585,6 +630,11 @@ def main():
         extra["backbone"] = bb
         for k, v in bb.items():
             print(f"[bench] {k}: {v}", file=sys.stderr, flush=True)
+        ho = host_overhead(pkg, dev)
+        ho["method"] = (f"eager host µs per call: {HOST_CALLS} back-to-back calls without a synchronisation, config 1 "
+                        f"inputs (GEMV 2x1024x1024), median of 5 samples")
+        extra["host_overhead"] = ho
+        print(f"[bench] host overhead: {ho}", file=sys.stderr, flush=True)
         line["extra"] = extra
     if not args.no_cpu:
         us_cpu, cores, n = cpu_baseline(w2, calls=100000, budget_s=10.0)

@@ -32,7 +32,7 @@ SplitFn pick_combine(int D, int G) {
   return nullptr;
 }
 
-using WaveFn = void (*)(const Params, int);
+using WaveFn = void (*)(const Params);
 
 WaveFn pick_wave(int D) {
   if (D == 128) return gqa_wave_kernel<128>;
@@ -171,6 +171,7 @@ Params base_params(const bz_gqa_decode_args* a, const int32_t* seq_lens, const i
   p.B = a->batch;
   p.NH = a->num_q_heads;
   p.NKV = a->num_kv_heads;
+  p.G = a->num_q_heads / a->num_kv_heads;
   p.cap = a->capacity;
   p.splits = 1;
   return p;
@@ -186,24 +187,33 @@ bool wave_out_aligned(const bz_gqa_decode_args* a) {
 int launch_wave(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_lens, const int32_t* kv_start) {
   const WaveFn fn = pick_wave(a->head_dim);
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
-  if ((int64_t)rows_of(a) * a->num_q_heads > INT32_MAX) return BZ_ERR_SHAPE;  // one workgroup per wave: grid.x
+  if (rows_of(a) > 65535) return BZ_ERR_SHAPE;  // one workgroup per wave: grid (G, NKV, rows), grid.z <= 65535
   const Params p = base_params(a, seq_lens, kv_start);
-  const int waves = rows_of(a) * a->num_q_heads;
-  hipLaunchKernelGGL(fn, dim3(waves), dim3(kWave), 0, stream, p, waves);
+  hipLaunchKernelGGL(fn, dim3(a->num_q_heads / a->num_kv_heads, a->num_kv_heads, rows_of(a)), dim3(kWave), 0, stream,
+                     p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
-// The automatic route to the wave kernel: rows of at most kWaveRouteLen positions in groups of four or more q heads
-// (the reference's depth transformer: 8 q / 2 KV heads, at most 17 positions), with nothing asked explicitly (split
-// count, combine mode) and no mask. There the split kernel's waves each run the dot products and softmax of all G
-// heads in series, and one wave per q head is faster (B2 8/2 D128, per launch: lengths 2..17 2.9 against 3.8 us;
-// 32 positions 3.45 against 3.89 with the rows in the L2, as a depth step's freshly written rows are). Cold rows
-// would favour the split kernel (32 positions: 4.25 against 3.90 us), since each q head reads its K/V itself.
-constexpr int kWaveRouteLen = 32;
+// The automatic route to the wave kernel: groups of two or more q heads over short rows, with nothing asked explicitly
+// (split count, combine mode) and no mask. The split kernel's waves each run the dot products and softmax of all G
+// heads in series, while the wave kernel gives each q head a wave whose first two K/V tiles (2 * 2048 / D positions)
+// are loaded before its range is known. Measured per launch, 16 launches in a HIP graph over rows in the L2 (as a
+// depth step's freshly written rows are), B2, 2 or 8 kv heads:
+//   D 128, G 2: 17 positions 2.52 against 2.65 us, 32: 2.69 / 2.70, 48: 3.32 / 2.98 (the split kernel wins)
+//   D 128, G 4: 17 positions 2.55 / 3.43, 32: 2.71 / 3.53, 64: 3.94 / 4.09, 128: 6.43 / 5.46
+//   D 64,  G 2: 32 positions 2.17 / 2.51, 64: 2.65 / 2.75, 128: 3.74 / 3.12
+//   D 64,  G 4: 64 positions 2.66 / 3.29, 128: 3.79 / 3.80
+//   G 1: the split kernel from 17 positions on (D 128: 2.51 / 2.38)
+// so the route takes rows of at most two tiles for G = 2 and four tiles for G >= 4 (positions: max_seq_len, else the
+// capacity). The reference's depth transformer (8 q / 2 KV heads, D 128, at most 17 positions) is on it.
+int wave_route_len(int D, int G) {
+  const int tile = 2048 / D;  // positions per K/V tile of attend_wave
+  return G >= 4 ? 4 * tile : (G >= 2 ? 2 * tile : 0);
+}
 
 bool wave_route(const bz_gqa_decode_args* a, int mask_kind, const bz_gqa_decode_fused_args* f) {
   return f == nullptr && mask_kind == BZ_MASK_NONE && a->num_splits == 0 && a->combine == BZ_COMBINE_AUTO &&
-         a->num_q_heads >= 4 * a->num_kv_heads && effective_len(a->capacity, a->max_seq_len) <= kWaveRouteLen &&
+         effective_len(a->capacity, a->max_seq_len) <= wave_route_len(a->head_dim, a->num_q_heads / a->num_kv_heads) &&
          wave_out_aligned(a);
 }
 

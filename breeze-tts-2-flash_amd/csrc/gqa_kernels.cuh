@@ -51,6 +51,7 @@ struct Params {
   uint16_t* out;
   int64_t o_sb, o_sh, o_st;
   int B, NH, NKV, cap, splits, min_chunk;
+  int G;             // NH / NKV
   int mask_kind;     // bz_mask_dtype of mask (for the merge kernel, which is not templated on it)
   int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
   float* part_acc;   // [B * T, NKV, splits, G * D]  unnormalised sum_p 2^(s_p - m) v_p
@@ -152,10 +153,13 @@ __device__ __forceinline__ uint4 lane_fetch4(const uint4& x, int src_lane) {
 
 // Clamp the row's range so that no access can leave [0, capacity).
 __device__ __forceinline__ void row_range(const Params& p, int b, int& start, int& end) {
+  // both loads are issued before either is waited for: without kv_start the second one reads seq_lens again and its
+  // value is dropped (a conditional load would wait for the first before issuing the second)
+  const int32_t* ks = p.kv_start ? p.kv_start : p.seq_lens;
   int e = p.seq_lens[b];
+  int s = ks[b];
   e = e < 0 ? 0 : (e > p.cap ? p.cap : e);
-  int s = p.kv_start ? p.kv_start[b] : 0;
-  s = s < 0 ? 0 : (s > e ? e : s);
+  s = p.kv_start == nullptr || s < 0 ? 0 : (s > e ? e : s);
   start = s;
   end = e;
 }
@@ -377,21 +381,21 @@ __device__ __forceinline__ void load_tile(Tile<PPT>& t, const Spans& sp, int pos
 // Fold one tile into the running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP row sum,
 // scaled by scale * log2(e); online softmax in base 2 with one max per wave (m is wave-uniform, l and acc per row);
 // then P.V in fp32 on the unpacked V registers.
-// A slot whose row lies past hi is skipped (the condition is uniform over the row's lanes, so the DPP sum, which
-// reads only lanes of the same row, never sees a skipped lane).
+// A slot whose row lies past hi (or, with LO, before lo) is skipped (the condition is uniform over the row's lanes, so
+// the DPP sum, which reads only lanes of the same row, never sees a skipped lane).
 // Fused prologue: the slot newpos (>= 0 only in the workgroup whose chunk holds it) takes the new k / v computed in
 // registers; the cache write of this call is not read back.
-template <int LPR, int ROWS, int G, int PPT, int MK, bool FUSED>
+template <int LPR, int ROWS, int G, int PPT, int MK, bool FUSED, bool LO = false>
 __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G], float scale_log2, float (&m)[G],
                                              float (&l)[G], float (&acc)[G][8], int pos0, int hi, int newpos,
-                                             const uint4& knew, const uint4& vnew) {
+                                             const uint4& knew, const uint4& vnew, int lo = 0) {
   float s[G][PPT];
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
 #pragma unroll
     for (int g = 0; g < G; ++g) s[g][i] = -INFINITY;
     const int pos = pos0 + ROWS * i;
-    if (pos < hi) {
+    if (pos < hi && (!LO || pos >= lo)) {
       if (FUSED && pos == newpos) {
         t.k[i] = knew;
         t.v[i] = vnew;
@@ -441,7 +445,7 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
   }
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-    if (pos0 + ROWS * i < hi) {
+    if (pos0 + ROWS * i < hi && (!LO || pos0 + ROWS * i >= lo)) {
       float vf[8];
       unpack8(t.v[i], vf);
 #pragma unroll

@@ -3,7 +3,7 @@
 // stage gives each warp one (row, q head) pair over at most 17 cached positions). Here too one wave owns one (row,
 // q head), and the K/V bytes go from the cache straight into VGPRs (no LDS staging, no barrier), so the caller may run
 // it from any wave of any workgroup, with other waves busy elsewhere. Any length works; it is built for short ones
-// (one or two tiles of 2 * 64 / (D / 8) positions).
+// (two tiles of 4 * 64 / (D / 8) positions: 32 at head_dim 128).
 //
 // The q heads of a group read the same K/V bytes, each through its own wave (from the L2 after the first). A wave that
 // owned a whole group instead, sharing each K/V load among its G heads, measured slower: its serial chain of dot
@@ -12,8 +12,8 @@
 //
 // The arithmetic is the split kernel's (gqa_kernels.cuh: load_tile, consume_tile): bf16 dot2 products with fp32
 // accumulation, online softmax in base 2 with one running max per wave, fp32 P.V; then the rows of the wave are summed
-// (the max is wave-uniform, so plain sums merge them) and the first row writes bf16(acc / sum), or 0 for an empty
-// range.
+// (the max is wave-uniform, so plain sums merge them) and the first row writes bf16(acc * (1 / sum)), or 0 for an
+// empty range.
 #pragma once
 
 #include "gqa_kernels.cuh"
@@ -26,7 +26,7 @@ struct WaveAttention {
   const uint16_t* k;   // K and V of its kv head in this row: position p at k + p * kv_ss (16-byte aligned rows)
   const uint16_t* v;
   int64_t kv_ss;
-  int start, end;      // attended positions [start, end), 0 <= start; end * kv_ss * 2 < 2^31
+  int cap;             // positions [0, cap) of k / v are readable; cap * kv_ss * 2 < 2^31
   float scale_log2;    // softmax scale * log2(e)
   uint16_t* out;       // D bf16 (16-byte aligned)
 };
@@ -43,31 +43,50 @@ __device__ __forceinline__ float rows_total(float x) {
   return x + y;
 }
 
-// Called by all 64 lanes of one wave (wave-uniform arguments).
-template <int D>
-__device__ void attend_wave(const WaveAttention& a) {
+// Called by all 64 lanes of one wave (wave-uniform arguments). range(start, end) gives the attended positions
+// [start, end), 0 <= start <= end <= cap; it is called once the first K / V loads are issued, so that whatever memory
+// it reads is in flight together with them.
+//
+// The wave reads K / V in tiles of TP positions at absolute positions (tile k holds [k TP, (k + 1) TP)) and masks
+// what lies outside [start, end). The first two tiles (positions [0, 2 TP): 32 at head_dim 128, 64 at head_dim 64,
+// every length the automatic route sends here) are loaded together with q before the range is known: in a launch
+// this short the range (a load of seq_lens that depends on the kernel arguments) and the K / V tiles were two
+// dependent memory round trips, and now they overlap. A range past those tiles reloads them at its own start; longer
+// ranges stream further tiles two at a time.
+template <int D, class Range>
+__device__ void attend_wave(const WaveAttention& a, Range range) {
   constexpr int G = 1;  // one q head per wave: the group size of the shared tile code (consume_tile)
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  constexpr int LPR = D / 8, RPW = kWave / LPR, PPT = 2, TP = RPW * PPT;
+  constexpr int LPR = D / 8, RPW = kWave / LPR, PPT = 4, TP = RPW * PPT;
   const int lane = __lane_id(), r = lane / LPR, c = lane % LPR;
   // the arguments are wave-uniform; taking them through a scalar register keeps the buffer resources and the loop
   // bounds scalar whatever the caller derived them from
-  const int start = wave_uniform(a.start), end = max(start, wave_uniform(a.end));
   const int64_t kv_ss = wave_uniform(a.kv_ss);
+  const int cap = wave_uniform(a.cap);
   uint16_t* const outp = wave_uniform(a.out);
 
-  // q first: loads complete in issue order, so the first tile's q.k waits for q and that tile alone
-  const Rsrc rq = span_rsrc(wave_uniform(a.q), D * 2);
-  const uint4 qp[G] = {__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)(16 * c), 0, 0))};
   Spans sp;
   sp.row_bytes = (uint32_t)kv_ss * 2;
   sp.lane_off = 16 * c;
-  sp.k = span_rsrc(wave_uniform(a.k), end * (int)sp.row_bytes);
-  sp.v = span_rsrc(wave_uniform(a.v), end * (int)sp.row_bytes);
+  sp.k = span_rsrc(wave_uniform(a.k), cap * (int)sp.row_bytes);
+  sp.v = span_rsrc(wave_uniform(a.v), cap * (int)sp.row_bytes);
   Tile<PPT> ta, tb;
-  load_tile<RPW, PPT, BZ_MASK_NONE>(ta, sp, start + r);
-  load_tile<RPW, PPT, BZ_MASK_NONE>(tb, sp, start + TP + r);
+  load_tile<RPW, PPT, BZ_MASK_NONE>(ta, sp, r);
+  load_tile<RPW, PPT, BZ_MASK_NONE>(tb, sp, TP + r);
+  const Rsrc rq = span_rsrc(wave_uniform(a.q), D * 2);
+  const uint4 qp[G] = {__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)(16 * c), 0, 0))};
   __builtin_amdgcn_sched_barrier(0);
+
+  int start = 0, end = 0;
+  range(start, end);
+  start = wave_uniform(start);
+  end = max(start, wave_uniform(end));
+  int t0 = 0;
+  if (start >= 2 * TP) {  // only through bz_gqa_decode_wave, which takes any range
+    t0 = start - start % TP;
+    load_tile<RPW, PPT, BZ_MASK_NONE>(ta, sp, t0 + r);
+    load_tile<RPW, PPT, BZ_MASK_NONE>(tb, sp, t0 + TP + r);
+  }
 
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -78,22 +97,24 @@ __device__ void attend_wave(const WaveAttention& a) {
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
   }
   const uint4 none = make_uint4(0, 0, 0, 0);
-  for (int t0 = start; t0 < end; t0 += 2 * TP) {
-    consume_tile<LPR, RPW, G, PPT, BZ_MASK_NONE, false>(ta, qp, a.scale_log2, m, l, acc, t0 + r, end, -1, none, none);
+  for (;; t0 += 2 * TP) {
+    consume_tile<LPR, RPW, G, PPT, BZ_MASK_NONE, false, true>(ta, qp, a.scale_log2, m, l, acc, t0 + r, end, -1, none,
+                                                              none, start);
     if (t0 + TP >= end) break;
-    load_tile<RPW, PPT, BZ_MASK_NONE>(ta, sp, t0 + 2 * TP + r);
-    consume_tile<LPR, RPW, G, PPT, BZ_MASK_NONE, false>(tb, qp, a.scale_log2, m, l, acc, t0 + TP + r, end, -1, none,
-                                                        none);
-    load_tile<RPW, PPT, BZ_MASK_NONE>(tb, sp, t0 + 3 * TP + r);
+    if (t0 + 2 * TP < end) load_tile<RPW, PPT, BZ_MASK_NONE>(ta, sp, t0 + 2 * TP + r);
+    consume_tile<LPR, RPW, G, PPT, BZ_MASK_NONE, false, true>(tb, qp, a.scale_log2, m, l, acc, t0 + TP + r, end, -1,
+                                                              none, none, start);
+    if (t0 + 2 * TP >= end) break;
+    if (t0 + 3 * TP < end) load_tile<RPW, PPT, BZ_MASK_NONE>(tb, sp, t0 + 3 * TP + r);
   }
 
+  // one reciprocal of the row total instead of a division per element (v_rcp_f32, within 1 ulp; exact for the powers
+  // of two, so a single attended position still returns its V row unchanged)
   const float L = rows_total<LPR>(l[0]);
+  const float inv = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
   float o[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float A = rows_total<LPR>(acc[0][j]);
-    o[j] = L > 0.f ? A / L : 0.f;
-  }
+  for (int j = 0; j < 8; ++j) o[j] = rows_total<LPR>(acc[0][j]) * inv;
   if (r == 0) {
     uint4 w;
     w.x = pack_bf16x2(o[0], o[1]);
@@ -107,22 +128,44 @@ __device__ void attend_wave(const WaveAttention& a) {
 // One wave per (row, token, q head) of a bz_gqa_decode call: range from seq_lens / kv_start (token t of T attends up
 // to itself), then attend_wave. One wave per workgroup, so the waves spread over as many CUs as there are
 // (config-5 frame with one wave per kv head: 102 us against 111 with four waves per workgroup, 108 with two).
+// Grid (group size G, kv heads, rows * T): the launch covers exactly the waves, and the head indices need no division.
 template <int D>
-__global__ void __launch_bounds__(kWave) gqa_wave_kernel(const bz::Params p, int waves) {
-  const int gi = blockIdx.x;
-  if (gi >= waves) return;
-  const int hq = gi % p.NH, z = gi / p.NH;  // z = row * T + token
-  const int h = hq / (p.NH / p.NKV);        // its kv head (repeat_kv)
-  const int b = z / p.T, tok = z - b * p.T;
+__global__ void __launch_bounds__(kWave) gqa_wave_kernel(const bz::Params p) {
+  // every kernel argument the wave reads is loaded before any of them is used, so that the loads go out together:
+  // one round trip to the argument buffer instead of one per group of dependent uses
+  const uint16_t* const q = p.q;
+  const int64_t q_sb = p.q_sb, q_sh = p.q_sh, q_st = p.q_st;
+  const uint16_t* const k = p.k;
+  const uint16_t* const v = p.v;
+  const int64_t kv_sb = p.kv_sb, kv_sh = p.kv_sh, kv_ss = p.kv_ss;
+  const int32_t* const lens = p.seq_lens;
+  const int32_t* const starts = p.kv_start;
+  uint16_t* const out = p.out;
+  const int64_t o_sb = p.o_sb, o_sh = p.o_sh, o_st = p.o_st;
+  const int T = p.T, cap = p.cap, G = p.G;
+  const float scale_log2 = p.scale_log2;
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int h = blockIdx.y, hq = h * G + blockIdx.x, z = blockIdx.z;  // z = row * T + token
+  const int b = T == 1 ? z : z / T, tok = z - b * T;
   WaveAttention a;
-  a.q = p.q + (int64_t)b * p.q_sb + (int64_t)tok * p.q_st + (int64_t)hq * p.q_sh;
-  a.k = p.k + (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh;
-  a.v = p.v + (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh;
-  a.kv_ss = p.kv_ss;
-  token_range(p, b, tok, a.start, a.end);
-  a.scale_log2 = p.scale_log2;
-  a.out = p.out + (int64_t)b * p.o_sb + (int64_t)tok * p.o_st + (int64_t)hq * p.o_sh;
-  attend_wave<D>(a);
+  a.q = q + (int64_t)b * q_sb + (int64_t)tok * q_st + (int64_t)hq * q_sh;
+  a.k = k + (int64_t)b * kv_sb + (int64_t)h * kv_sh;
+  a.v = v + (int64_t)b * kv_sb + (int64_t)h * kv_sh;
+  a.kv_ss = kv_ss;
+  a.cap = cap;
+  a.scale_log2 = scale_log2;
+  a.out = out + (int64_t)b * o_sb + (int64_t)tok * o_st + (int64_t)hq * o_sh;
+  attend_wave<D>(a, [&](int& start, int& end) {
+    // row_range and token_range on the values above; both loads are issued before either is waited for (without
+    // kv_start the second reads seq_lens again and its value is dropped)
+    int e = lens[b];
+    int s = (starts ? starts : lens)[b];
+    e = e < 0 ? 0 : (e > cap ? cap : e);
+    s = starts == nullptr || s < 0 ? 0 : (s > e ? e : s);
+    start = s;
+    end = max(s, e - (T - 1 - tok));
+  });
 }
 
 }  // namespace

@@ -112,9 +112,10 @@ typedef struct bz_gqa_decode_args {
 
 /* GQA decode attention. Replaces the reference op attn_decode (flash/csrc/bb_attn.cu:416-429, pybind :463-465)
    with the north-star signature (q, k_cache, v_cache, seq_lens, scale) -> out; kv_start carries the left-padding
-   start the reference encodes in its interval mask (backbone_graph.py:239-252). With num_splits 0, combine AUTO, no
-   mask, groups of 4 or more q heads per kv head and at most 32 positions (max_seq_len, else capacity) it runs the
-   kernel of bz_gqa_decode_wave (the depth transformer's shape); otherwise the split kernel. */
+   start the reference encodes in its interval mask (backbone_graph.py:239-252). With num_splits 0, combine AUTO and
+   no mask, on short rows (max_seq_len, else capacity: at most 4096 / head_dim positions for 2 q heads per kv head,
+   8192 / head_dim for 4 or more) it runs the kernel of bz_gqa_decode_wave (the depth transformer's shape); otherwise
+   the split kernel. */
 int bz_gqa_decode(const bz_gqa_decode_args* args, hipStream_t stream);
 
 /* bz_gqa_decode without a workspace and without any allocation: args->workspace and args->workspace_bytes are ignored

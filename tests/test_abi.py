@@ -263,7 +263,7 @@ def test_rmsnorm_validation(lib):
     (dict(out=0x40008), -4), (dict(out_stride_h=132), -4), (dict(out_stride_b=16 * 128 + 4), -4),
     (dict(tokens_per_row=2, q_stride_t=128 * 16, out_stride_t=68), -4),
     (dict(k_cache=0x100008), -4),
-    (dict(batch=65535, num_q_heads=8 * 65535, num_kv_heads=65535), -2),  # rows x q heads waves > 2^31 - 1
+    (dict(batch=65536), -2),  # rows > 65535: the grid's z dimension
 ])
 def test_wave_validation(lib, K, over, code):
     a = _good_args(K, **over)

@@ -142,21 +142,36 @@ def test_argument_errors(device):
         gqa_decode_wave(q[..., :96].contiguous(), k[..., :96].contiguous(), k[..., :96].contiguous(), lens, 0.1)
 
 
-def test_gqa_decode_routes_short_wide_groups(device):
-    """bz_gqa_decode runs the wave kernel for groups of >= 4 q heads over <= 32 positions when nothing is asked
-    explicitly: its output is then bit-identical to bz_gqa_decode_wave's. Past 32 positions, or with an explicit split
-    count, it runs the split kernel (one split at these sizes)."""
-    rng = np.random.default_rng(77)
-    B, NH, NKV, D = 2, 8, 2, 128
-    for cap, routed in ((17, True), (32, True), (33, False), (64, False)):
-        q = bf16(rng.standard_normal((B, NH, D)), device)
-        k = bf16(rng.standard_normal((B, NKV, cap, D)), device)
-        v = bf16(rng.standard_normal((B, NKV, cap, D)), device)
-        lens = i32([cap, cap - 5], device)
-        auto = gqa_decode(q, k, v, lens, D ** -0.5)
-        wave = gqa_decode_wave(q, k, v, lens, D ** -0.5)
-        one = gqa_decode(q, k, v, lens, D ** -0.5, num_splits=1)
-        torch.cuda.synchronize()
-        check(auto[:, None], q[:, :, None], k, v, [cap, cap - 5], D ** -0.5, what=f"auto cap={cap}")
-        same = wave if routed else one
-        assert torch.equal(auto.view(torch.int16), same.view(torch.int16)), f"cap={cap} routed={routed}"
+# (head_dim, q heads per kv head, capacity, routed): the wave kernel takes rows of at most 4096 / head_dim positions
+# for 2 q heads per kv head and 8192 / head_dim for 4 or more; 1 q head per kv head always takes the split kernel
+ROUTES = [(128, 4, 17, True), (128, 4, 64, True), (128, 4, 65, False), (128, 8, 64, True), (128, 2, 32, True),
+          (128, 2, 33, False), (128, 1, 8, False), (64, 2, 64, True), (64, 2, 65, False), (64, 4, 128, True),
+          (64, 4, 129, False)]
+
+
+@pytest.mark.parametrize("D,G,cap,routed", ROUTES)
+def test_gqa_decode_routes_short_wide_groups(device, D, G, cap, routed):
+    """bz_gqa_decode runs the wave kernel on short rows in groups of two or more q heads when nothing is asked
+    explicitly: its output is then bit-identical to bz_gqa_decode_wave's. Past the route's length, for single-head
+    groups, or with an explicit split count, it runs the split kernel (one split at these sizes)."""
+    rng = np.random.default_rng(77 + cap)
+    B, NKV = 2, 2
+    NH = NKV * G
+    q = bf16(rng.standard_normal((B, NH, D)), device)
+    k = bf16(rng.standard_normal((B, NKV, cap, D)), device)
+    v = bf16(rng.standard_normal((B, NKV, cap, D)), device)
+    lens = i32([cap, cap - 5], device)
+    auto = gqa_decode(q, k, v, lens, D ** -0.5)
+    wave = gqa_decode_wave(q, k, v, lens, D ** -0.5)
+    one = gqa_decode(q, k, v, lens, D ** -0.5, num_splits=1)
+    torch.cuda.synchronize()
+    check(auto[:, None], q[:, :, None], k, v, [cap, cap - 5], D ** -0.5, what=f"auto cap={cap}")
+    same = wave if routed else one
+    assert torch.equal(auto.view(torch.int16), same.view(torch.int16)), f"D={D} G={G} cap={cap} routed={routed}"
+    # the wave kernel needs no workspace and the split kernel does: a too-small one shows which route was taken
+    tiny = torch.zeros(256, dtype=torch.uint8, device=device)
+    if routed:
+        gqa_decode(q, k, v, lens, D ** -0.5, workspace=tiny)
+    else:
+        with pytest.raises(RuntimeError, match="workspace"):
+            gqa_decode(q, k, v, lens, D ** -0.5, workspace=tiny)
