@@ -287,6 +287,42 @@ def _gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_se
     return out
 
 
+def _check_probs(probs: torch.Tensor, a, dev) -> None:
+    n = a.batch * a.num_q_heads * a.capacity
+    _check(probs.dtype == torch.float32 and probs.device == dev and probs.is_contiguous() and probs.numel() >= n,
+           f"probs (dbg) must be a contiguous float32 tensor on the query's device with at least B * NH * capacity = "
+           f"{n} elements")
+
+
+def gqa_decode_probs(q: torch.Tensor, k_cache: torch.Tensor, seq_lens: torch.Tensor | None, scale: float,
+                     probs: torch.Tensor | None = None, *, kv_start: torch.Tensor | None = None,
+                     mask: torch.Tensor | None = None) -> torch.Tensor:
+    """The softmax probabilities of the gqa_decode call with these arguments (bz_gqa_decode_probs): float32
+    [B, NH, capacity], each bf16(exp(s - max) / sum) inside the row's range and 0 at excluded positions and outside
+    it. seq_lens None: the range comes from the mask, as in gqa_decode_masked. The reference's optional dbg output of
+    attn_decode (bb_attn.cu:74, :288-289); a verification path, not a fast one. q: [B, NH, D] (one query token)."""
+    _check(q.dim() == 3 or (q.dim() == 4 and q.size(2) == 1), "gqa_decode_probs takes one query token per row")
+    a, _ = _fill_args(q, k_cache, k_cache, scale, None, 0, 0, "auto")
+    dev = q.device
+    if seq_lens is not None:
+        a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
+        a.kv_start = _int32_rows(kv_start, a.batch, "kv_start", dev).data_ptr() if kv_start is not None else None
+    else:
+        _check(mask is not None, "gqa_decode_probs needs seq_lens or a mask")
+    if mask is not None:
+        _check(mask.device == dev, "mask must be on the query's device")
+        a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
+        a.mask = mask.data_ptr()
+    if probs is None:
+        probs = torch.empty(a.batch, a.num_q_heads, a.capacity, dtype=torch.float32, device=dev)
+    _check_probs(probs, a, dev)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        kernels.check(kernels.load().bz_gqa_decode_probs(ctypes.byref(a), ctypes.c_void_p(probs.data_ptr()),
+                                                         ctypes.c_void_p(stream)), "bz_gqa_decode_probs")
+    return probs
+
+
 def mask_interval(mask: torch.Tensor, capacity: int, batch: int | None = None,
                   seq_lens: torch.Tensor | None = None,
                   kv_start: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -339,8 +375,10 @@ def gqa_decode_fused(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
 
 
 def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
-                      seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace) -> torch.Tensor:
-    """gqa_decode_fused's call through the C ABI."""
+                      seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace,
+                      probs=None) -> torch.Tensor:
+    """gqa_decode_fused's call through the C ABI; with probs (float32 [B, NH, capacity]), then the step's softmax
+    probabilities into it (bz_gqa_decode_fused_probs: the reference's dbg output of attn_decode_fused)."""
     _check(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.dtype == torch.bfloat16,
            "qkv must be a bf16 [B, (NH + 2 NKV) * D] tensor with a contiguous last dim")
     _check(k_cache.dim() == 4, "k_cache must be [B, NKV, capacity, D]")
@@ -382,4 +420,9 @@ def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
         stream = torch.cuda.current_stream(dev).cuda_stream
         kernels.check(kernels.load().bz_gqa_decode_fused(ctypes.byref(f), ctypes.c_void_p(stream)),
                       "bz_gqa_decode_fused")
+        if probs is not None:
+            _check_probs(probs, a, dev)
+            kernels.check(kernels.load().bz_gqa_decode_fused_probs(ctypes.byref(f), ctypes.c_void_p(probs.data_ptr()),
+                                                                   ctypes.c_void_p(stream)),
+                          "bz_gqa_decode_fused_probs")
     return out

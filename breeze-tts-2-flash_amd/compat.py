@@ -5,30 +5,43 @@ flash/csrc/bb_attn.cu:463-465 (host function :416-429). The reference takes the 
 mask (valid = [pad_lens[b], position], everything else finfo.min; backbone_graph.py:239-252) and needs four
 caller-owned workspaces. Here the range is derived from the mask on the device (bz_gqa_decode_masked) and the
 library's own cached workspace is used; scores / cmax / part / counters are accepted for signature compatibility and
-left untouched. The reference's optional dbg output (bf16-rounded probabilities, bb_attn.cu:288) has no caller
-(flash/backbone.py:123-124 passes none) and is not produced: passing one raises.
+left untouched. The reference's optional dbg output (float32 [B, NH, S], the bf16-rounded softmax probabilities,
+bb_attn.cu:288-289, checked at :401-405) is produced when given, by a second launch after the attention
+(bz_gqa_decode_probs / bz_gqa_decode_fused_probs); the reference's decode step passes none (flash/backbone.py:123-124).
 """
 from __future__ import annotations
 
 import torch
 
-from .attention import gqa_decode_fused, gqa_decode_masked
+from . import attention
+from .attention import gqa_decode_fused, gqa_decode_masked, gqa_decode_probs
+
+
+def _check_dbg(dbg: torch.Tensor, B: int, NH: int, S: int, device, what: str) -> None:
+    """The reference's dbg check (bb_attn.cu:401-405), made before anything is launched."""
+    if not (dbg.dtype == torch.float32 and dbg.is_contiguous() and dbg.device == device and dbg.numel() >= B * NH * S):
+        raise RuntimeError(f"{what}: dbg must be a contiguous float32 tensor on the query's device with at least "
+                           f"B * NH * S = {B * NH * S} elements")
 
 
 def attn_decode(query: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, mask: torch.Tensor, scaling: float,
                 scores=None, cmax=None, part=None, counters=None, out: torch.Tensor | None = None,
                 dbg: torch.Tensor | None = None) -> torch.Tensor:
     """query [B, NH, 1, D] bf16; kc/vc [B, NKV, S, D] bf16 (stride(3) == 1); mask [B or 1, 1, 1, >= S] bf16/fp32;
-    out [B, 1, NH, D] bf16 contiguous (the eager attn_output.transpose(1, 2) layout). Returns out."""
-    if dbg is not None:
-        raise RuntimeError("attn_decode: the dbg probabilities output is not supported")
+    out [B, 1, NH, D] bf16 contiguous (the eager attn_output.transpose(1, 2) layout); dbg, when given, float32
+    contiguous with at least B * NH * S elements, receives the probabilities. Returns out."""
     if query.dim() != 4 or query.size(2) != 1:
         raise RuntimeError(f"attn_decode: query must be [B, NH, 1, D], got {tuple(query.shape)}")
     if out is None:
         out = torch.empty(query.size(0), 1, query.size(1), query.size(3), dtype=torch.bfloat16, device=query.device)
     if mask.dim() != 4 or mask.size(2) != 1:
         raise RuntimeError(f"attn_decode: mask must be [B or 1, 1, 1, S], got {tuple(mask.shape)}")
-    return gqa_decode_masked(query, kc, vc, mask, scaling, out)
+    if dbg is not None:
+        _check_dbg(dbg, query.size(0), query.size(1), kc.size(2), query.device, "attn_decode")
+    gqa_decode_masked(query, kc, vc, mask, scaling, out)
+    if dbg is not None:
+        gqa_decode_probs(query, kc, None, scaling, dbg, mask=mask)
+    return out
 
 
 def attn_decode_fused(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, cos: torch.Tensor,
@@ -38,13 +51,16 @@ def attn_decode_fused(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor,
     """The reference's fused decode step, pybind signature flash/csrc/bb_attn.cu:466-469 (host function :433-460),
     as called by flash/backbone.py:123-124: qkv [B, (NH + 2 NKV) * 128] raw projections, qn_w/kn_w [128],
     cos/sin [B, 1, 128], kc/vc the layer's StaticCache tensors (written at slot cache_pos[0]), mask the interval
-    mask, out [B, 1, NH, 128]. The four workspaces are accepted and left untouched; dbg is not supported."""
-    if dbg is not None:
-        raise RuntimeError("attn_decode_fused: the dbg probabilities output is not supported")
+    mask, out [B, 1, NH, 128]. The four workspaces are accepted and left untouched; dbg, when given (float32,
+    contiguous, at least B * NH * S elements), receives the step's probabilities, its own new position included."""
     if out is None:
         NKV, D = kc.size(1), kc.size(3)
         NH = qkv.size(1) // D - 2 * NKV
         out = torch.empty(qkv.size(0), 1, NH, D, dtype=torch.bfloat16, device=qkv.device)
     if mask.dim() != 4 or mask.size(2) != 1:
         raise RuntimeError(f"attn_decode_fused: mask must be [B or 1, 1, 1, S], got {tuple(mask.shape)}")
-    return gqa_decode_fused(qkv, qn_w, kn_w, eps, cos, sin, kc, vc, cache_pos, scaling, out, mask=mask)
+    if dbg is None:
+        return gqa_decode_fused(qkv, qn_w, kn_w, eps, cos, sin, kc, vc, cache_pos, scaling, out, mask=mask)
+    _check_dbg(dbg, qkv.size(0), out.size(2), kc.size(2), qkv.device, "attn_decode_fused")
+    return attention._gqa_decode_fused(qkv, qn_w, kn_w, eps, cos, sin, kc, vc, cache_pos, scaling, out, None, None,
+                                       mask, 0, 0, "auto", None, probs=dbg)

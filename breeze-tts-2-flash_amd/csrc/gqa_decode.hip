@@ -40,6 +40,23 @@ WaveFn pick_wave(int D) {
   return nullptr;
 }
 
+using ProbsFn = void (*)(const Params, float*);
+
+template <bool FUSED>
+ProbsFn pick_probs(int D, int mk) {
+  if (D == 128) {
+    if (mk == BZ_MASK_BF16) return gqa_probs_kernel<128, BZ_MASK_BF16, FUSED>;
+    if (mk == BZ_MASK_F32) return gqa_probs_kernel<128, BZ_MASK_F32, FUSED>;
+    return gqa_probs_kernel<128, BZ_MASK_NONE, FUSED>;
+  }
+  if (D == 64 && !FUSED) {
+    if (mk == BZ_MASK_BF16) return gqa_probs_kernel<64, BZ_MASK_BF16, false>;
+    if (mk == BZ_MASK_F32) return gqa_probs_kernel<64, BZ_MASK_F32, false>;
+    return gqa_probs_kernel<64, BZ_MASK_NONE, false>;
+  }
+  return nullptr;
+}
+
 bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 bool supported_dim(int D) { return D == 64 || D == 128; }
 
@@ -399,6 +416,30 @@ int check_fused(const bz_gqa_decode_fused_args* f) {
   return BZ_OK;
 }
 
+// The probabilities of bz_gqa_decode / bz_gqa_decode_fused (f != nullptr) with these arguments.
+int launch_probs(const bz_gqa_decode_args* a, const bz_gqa_decode_fused_args* f, float* probs, hipStream_t stream) {
+  if (probs == nullptr || (a->seq_lens == nullptr && a->mask == nullptr)) return BZ_ERR_NULL;
+  if (tokens_of(a) != 1) return BZ_ERR_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(probs) & 3) return BZ_ERR_ALIGNMENT;
+  const int mk = (a->mask == nullptr) ? BZ_MASK_NONE : a->mask_dtype;
+  if (a->mask != nullptr && mk != BZ_MASK_BF16 && mk != BZ_MASK_F32) return BZ_ERR_MASK_DTYPE;
+  const ProbsFn fn = f != nullptr ? pick_probs<true>(a->head_dim, mk) : pick_probs<false>(a->head_dim, mk);
+  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
+  Params p = base_params(a, a->seq_lens, a->seq_lens != nullptr ? a->kv_start : nullptr);
+  p.mask_kind = mk;
+  if (f != nullptr) {
+    p.qkv = static_cast<const uint16_t*>(f->qkv);
+    p.qkv_sb = f->qkv_stride_b;
+    p.qn_w = static_cast<const uint16_t*>(f->q_norm_weight);
+    p.eps = f->eps;
+    p.cos = static_cast<const uint16_t*>(f->cos);
+    p.sin = static_cast<const uint16_t*>(f->sin);
+    p.cs_sb = f->rope_stride_b;
+  }
+  hipLaunchKernelGGL(fn, dim3(a->num_q_heads, a->batch), dim3(kThreads), 0, stream, p, probs);
+  return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
+
 }  // namespace
 
 extern "C" {
@@ -460,6 +501,18 @@ __attribute__((visibility("default"))) int bz_gqa_decode_wave(const bz_gqa_decod
   if (a->mask != nullptr) return BZ_ERR_UNSUPPORTED;
   if (!wave_out_aligned(a)) return BZ_ERR_ALIGNMENT;
   return launch_wave(a, stream, a->seq_lens, a->kv_start);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_probs(const bz_gqa_decode_args* a, float* probs,
+                                                               hipStream_t stream) {
+  const int rc = check_common(a, true);
+  return rc != BZ_OK ? rc : launch_probs(a, nullptr, probs, stream);
+}
+
+__attribute__((visibility("default"))) int bz_gqa_decode_fused_probs(const bz_gqa_decode_fused_args* f, float* probs,
+                                                                     hipStream_t stream) {
+  const int rc = check_fused(f);
+  return rc != BZ_OK ? rc : launch_probs(&f->base, f, probs, stream);
 }
 
 __attribute__((visibility("default"))) int bz_mask_interval(const void* mask, int32_t mask_dtype,

@@ -717,6 +717,86 @@ __global__ void __launch_bounds__(kThreads) mask_range_kernel(const void* mask, 
   }
 }
 
+// Max (is_max) or sum of x over the kThreads threads of the workgroup; every thread gets the result.
+__device__ __forceinline__ float block_reduce(float x, bool is_max) {
+  __shared__ float s_red[kWaves];
+  x = is_max ? wave_max(x) : wave_sum(x);
+  __syncthreads();  // s_red may still be read by a previous reduction
+  if (threadIdx.x % kWave == 0) s_red[threadIdx.x / kWave] = x;
+  __syncthreads();
+  float r = s_red[0];
+#pragma unroll
+  for (int u = 1; u < kWaves; ++u) r = is_max ? fmaxf(r, s_red[u]) : r + s_red[u];
+  return r;
+}
+
+// The softmax probabilities of one decode step: the reference's optional dbg output (bb_attn.cu:74, :288-289,
+// :323-325), for verification. One workgroup per (q head, row) writes probs[(b * NH + hq) * cap + pos] for every
+// pos < cap: bf16(2^(s - M) / L) as fp32 inside the row's range, where s is the scaled score (plus the mask's value)
+// and M, L the max and the sum over the range, and 0 at excluded positions and outside the range. Three passes
+// through probs itself (scores, exponentials, normalised); each thread rereads only the positions it wrote.
+// FUSED: the step of bz_gqa_decode_fused, after it ran: q is the head's raw projection in qkv, normed and rotated
+// here as the fused kernel does it (norm_rope8, by the first D / 8 lanes, into LDS), and the cache already holds the
+// step's new k at cache_pos.
+template <int D, int MK, bool FUSED>
+__global__ void __launch_bounds__(kThreads) gqa_probs_kernel(const Params p, float* probs) {
+  static_assert(!FUSED || D == 128, "the fused prologue is built for head_dim 128");
+  const int hq = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int h = hq / p.G;
+  __shared__ __align__(16) uint16_t s_q[D];
+  const uint16_t* qh = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh;
+  if constexpr (FUSED) {
+    constexpr int LPR = D / 8;
+    if (tid < LPR) {  // one 16-lane DPP row of wave 0: lane c holds dims 8c .. 8c + 7
+      const uint4 x = *reinterpret_cast<const uint4*>(p.qkv + (int64_t)b * p.qkv_sb + (int64_t)hq * D + 8 * tid);
+      const uint4 w = *reinterpret_cast<const uint4*>(p.qn_w + 8 * tid);
+      const uint4 rc = *reinterpret_cast<const uint4*>(p.cos + (int64_t)b * p.cs_sb + 8 * tid);
+      const uint4 rs = *reinterpret_cast<const uint4*>(p.sin + (int64_t)b * p.cs_sb + 8 * tid);
+      *reinterpret_cast<uint4*>(s_q + 8 * tid) = norm_rope8<LPR>(x, w, rc, rs, p.eps, tid);
+    }
+    __syncthreads();
+    qh = s_q;
+  }
+  int start, end;
+  unit_range<kThreads>(p, b, 0, start, end);
+  float* const row = probs + ((int64_t)b * p.NH + hq) * p.cap;
+  const uint16_t* const kb = p.k + (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh;
+  float mx = -INFINITY;
+  for (int pos = tid; pos < p.cap; pos += kThreads) {
+    float s = -INFINITY;
+    if (pos >= start && pos < end) {
+      const uint16_t* const kr = kb + (int64_t)pos * p.kv_ss;
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < D; j += 8) {
+        const uint4 kv = *reinterpret_cast<const uint4*>(kr + j);
+        const uint4 qv = *reinterpret_cast<const uint4*>(qh + j);
+        d = dot2_bf16(qv.x, kv.x, d);
+        d = dot2_bf16(qv.y, kv.y, d);
+        d = dot2_bf16(qv.z, kv.z, d);
+        d = dot2_bf16(qv.w, kv.w, d);
+      }
+      s = d * p.scale_log2;
+      if (MK != BZ_MASK_NONE) {
+        const float m = load_mask<MK>(p.mask, (int64_t)b * p.m_sb + pos);
+        s = m > kExcluded ? fmaf(m, kLog2e, s) : -INFINITY;
+      }
+    }
+    row[pos] = s;
+    mx = fmaxf(mx, s);
+  }
+  const float M = block_reduce(mx, true);
+  const float mu = (M == -INFINITY) ? 0.f : M;
+  float sum = 0.f;
+  for (int pos = tid; pos < p.cap; pos += kThreads) {
+    const float e = fast_exp2(row[pos] - mu);  // 0 for -inf
+    row[pos] = e;
+    sum += e;
+  }
+  const float L = block_reduce(sum, false);
+  for (int pos = tid; pos < p.cap; pos += kThreads) row[pos] = L > 0.f ? bf16_to_f32(f32_to_bf16(row[pos] / L)) : 0.f;
+}
+
 // ---------------------------------------------------------------------------------------------- kernel tables
 
 template <int D, int G, int MK, int NT, bool FUSED>

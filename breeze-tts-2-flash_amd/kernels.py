@@ -31,13 +31,14 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # exported symbols and their ctypes signatures (include/bz_gqa_decode.h)
 EXPORTS = (
     "bz_gqa_decode", "bz_gqa_decode_masked", "bz_gqa_decode_fused", "bz_gqa_decode_workspace_size",
     "bz_gqa_decode_default_splits", "bz_status_string", "bz_gqa_decode_abi_version", "bz_gemv", "bz_rmsnorm",
     "bz_mask_interval", "bz_gqa_decode_wave", "bz_gqa_decode_build_id", "bz_gqa_decode_noalloc",
+    "bz_gqa_decode_probs", "bz_gqa_decode_fused_probs",
 )
 
 
@@ -185,6 +186,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_gqa_decode_wave.restype = ctypes.c_int
     lib.bz_gqa_decode_noalloc.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p]
     lib.bz_gqa_decode_noalloc.restype = ctypes.c_int
+    lib.bz_gqa_decode_probs.argtypes = [P(GqaDecodeArgs), ctypes.c_void_p, ctypes.c_void_p]
+    lib.bz_gqa_decode_probs.restype = ctypes.c_int
+    lib.bz_gqa_decode_fused_probs.argtypes = [P(GqaDecodeFusedArgs), ctypes.c_void_p, ctypes.c_void_p]
+    lib.bz_gqa_decode_fused_probs.restype = ctypes.c_int
     lib.bz_gqa_decode_build_id.argtypes = []
     lib.bz_gqa_decode_build_id.restype = ctypes.c_char_p
 

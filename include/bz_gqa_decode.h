@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define BZ_GQA_DECODE_ABI_VERSION 8
+#define BZ_GQA_DECODE_ABI_VERSION 9
 
 typedef enum bz_status {
   BZ_OK = 0,
@@ -181,6 +181,21 @@ int bz_gqa_decode_fused(const bz_gqa_decode_fused_args* args, hipStream_t stream
    real depth shape); on cold or long rows it is slower. No mask (BZ_ERR_UNSUPPORTED); out and its strides 16-byte
    aligned; workspace, num_splits, max_seq_len and combine are ignored; any row length works. */
 int bz_gqa_decode_wave(const bz_gqa_decode_args* args, hipStream_t stream);
+
+/* The softmax probabilities of the bz_gqa_decode call with these arguments: probs[(b * num_q_heads + h) * capacity + p]
+   = bf16(exp(s - max) / sum) as fp32 for position p inside row b's range (s the scaled score of q head h plus the
+   mask's value, max and sum over the range), 0 at excluded positions and outside the range; every p < capacity is
+   written. The range comes from seq_lens / kv_start, or with seq_lens NULL from the mask (as bz_gqa_decode_masked);
+   a mask, when given, is added inside the range. tokens_per_row must be 1; out and v_cache are not read or written;
+   probs is a float [batch, num_q_heads, capacity] device array, 4-byte aligned. Replaces the optional dbg output of
+   attn_decode / attn_decode_fused (flash/csrc/bb_attn.cu:74, :288-289, :323-325, :401-405): a verification path,
+   three passes over the row, not a fast one. */
+int bz_gqa_decode_probs(const bz_gqa_decode_args* args, float* probs, hipStream_t stream);
+
+/* bz_gqa_decode_probs for the fused step: the probabilities of the bz_gqa_decode_fused call with these arguments,
+   made after it (the cache then holds the step's new k at cache_pos; q is the raw projection in qkv, normed and
+   rotated as the fused kernel does it). The dbg output of attn_decode_fused (bb_attn.cu:288-289, :401-405). */
+int bz_gqa_decode_fused_probs(const bz_gqa_decode_fused_args* args, float* probs, hipStream_t stream);
 
 /* Per row b, the interval [kv_start[b], seq_lens[b]) of positions p < capacity whose additive mask value is > -1e30
    ([0, 0) for a row with none): the range bz_gqa_decode_masked and the mask form of bz_gqa_decode_fused derive on the

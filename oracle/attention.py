@@ -63,6 +63,38 @@ def decode_attention(q, k, v, seq_lens, scale: float, kv_start=None, mask=None) 
     return out
 
 
+def decode_probabilities(q, k, seq_lens, scale: float, kv_start=None, mask=None) -> np.ndarray:
+    """The softmax probabilities behind decode_attention: float64 [B, NH, capacity], softmax(q . k * scale + mask) over
+    each row's [start, end) with mask-excluded positions dropped, 0 outside the range, at excluded positions and for
+    rows with nothing to attend. The reference's optional dbg output of attn_decode (flash/csrc/bb_attn.cu:288-289)
+    holds these probabilities rounded to bf16."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    B, NH, D = q.shape
+    cap = k.shape[2]
+    probs = np.zeros((B, NH, cap), dtype=np.float64)
+    for b in range(B):
+        start, end = _row_range(b, seq_lens, kv_start, cap)
+        if end <= start:
+            continue
+        kh = expand_kv_heads(k[b, :, start:end], NH)
+        s = np.einsum("hd,hld->hl", q[b], kh) * scale
+        keep = np.ones(end - start, dtype=bool)
+        if mask is not None:
+            m = np.asarray(mask, dtype=np.float64)
+            m = m[b if m.shape[0] > 1 else 0, start:end]
+            keep = m > EXCLUDED
+            s = s + np.where(keep, m, 0.0)
+        if not keep.any():
+            continue
+        sk = s[:, keep]
+        e = np.exp(sk - sk.max(axis=1, keepdims=True))
+        p = np.zeros_like(s)
+        p[:, keep] = e / e.sum(axis=1, keepdims=True)
+        probs[b, :, start:end] = p
+    return probs
+
+
 def sdpa_fp32(q, k, v, seq_lens, scale: float, kv_start=None):
     """The north-star oracle verbatim: torch scaled_dot_product_attention in fp32 on the CPU with the KV heads
     expanded, sliced per row to [start, end). q [B, NH, D]; k, v [B, NKV, capacity, D] (torch tensors of any

@@ -373,9 +373,12 @@ def test_argument_errors(device):
         q96 = torch.zeros(2, 16, 96, dtype=torch.bfloat16, device=device)
         kv96 = torch.zeros(2, 8, 64, 96, dtype=torch.bfloat16, device=device)
         gqa_decode(q96, kv96, kv96, g.seq_lens, 0.1)
-    with pytest.raises(RuntimeError, match="dbg"):
+    out = torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(RuntimeError, match="dbg"):  # a dbg buffer smaller than B * NH * S, checked before any launch
         attn_decode(g.q[:, :, None], g.k, g.v, torch.zeros(2, 1, 1, 64, device=device), 0.1, None, None, None, None,
-                    torch.empty(2, 1, 16, 128, dtype=torch.bfloat16, device=device), dbg=torch.empty(1))
+                    out, dbg=torch.empty(1, device=device))
+    torch.cuda.synchronize()
+    assert not out.any(), "attn_decode ran before refusing its dbg buffer"
 
 
 # ---------------------------------------------------------------------------------------------- golden fixtures
