@@ -18,7 +18,7 @@ import torch
 
 from . import kernels
 
-_WS: dict = {}            # (device, stream, groups) -> workspace
+_WS: dict = {}            # (device index, raw stream handle, groups) -> workspace
 _WS_RETIRED: list = []    # workspaces replaced by larger ones (kept: a captured graph may still use them)
 _WS_LOCK = threading.Lock()
 
@@ -36,10 +36,18 @@ def _combine_code(combine) -> int:
 @functools.lru_cache(maxsize=1024)
 def _workspace_bytes(device_index: int, batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
                      capacity: int, num_splits: int, max_seq_len: int) -> int:
+    """bz_gqa_decode_workspace_size, computed with device device_index current (the default split count depends on
+    its CU count; -1: an explicit split count, no device needed)."""
     n = ctypes.c_size_t(0)
-    kernels.check(kernels.load().bz_gqa_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, capacity,
-                                                               num_splits, max_seq_len, ctypes.byref(n)),
-                  "bz_gqa_decode_workspace_size")
+
+    def size(_stream=None):
+        kernels.check(kernels.load().bz_gqa_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim,
+                                                                   capacity, num_splits, max_seq_len, ctypes.byref(n)),
+                      "bz_gqa_decode_workspace_size")
+    if device_index >= 0:
+        kernels.run_on(torch.device("cuda", device_index), size)
+    else:
+        size()
     return int(n.value)
 
 
@@ -69,17 +77,27 @@ def get_workspace(device: torch.device, batch: int, num_q_heads: int, num_kv_hea
     capacity or length. There is one per (device, stream, groups), because calls in flight on two streams must not
     share counters and partials. A call that needs more room replaces it with a zeroed one at least twice as large;
     the replaced one stays allocated (a captured graph may still use it), so the memory held stays under twice the
-    largest need. The first call on a stream that is being captured into a HIP graph allocates from the graph's pool
-    (its zero fill is then replayed with the graph); an eager call on the capture stream beforehand avoids that."""
-    n = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len)
-    stream = torch.cuda.current_stream(device).cuda_stream
-    key = (str(device), stream, batch * num_kv_heads)
+    largest need. A call without a workspace made while its stream is being captured into a HIP graph does not come
+    here: it runs on the library's static scratch (bz_gqa_decode_noalloc)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return kernels.run_on(torch.device("cuda", idx), lambda stream: _stream_workspace(
+        idx, stream, batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len))
+
+
+def _stream_workspace(idx: int, stream: int, batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                      capacity: int, num_splits: int, max_seq_len: int) -> torch.Tensor:
+    """get_workspace for device idx (current) and the raw handle of its current stream."""
+    n = _workspace_bytes(idx if num_splits == 0 else -1, batch, num_q_heads, num_kv_heads, head_dim, capacity,
+                         num_splits, max_seq_len)
+    key = (idx, stream, batch * num_kv_heads)
+    ws = _WS.get(key)
+    if ws is not None and ws.numel() >= n:
+        return ws
     with _WS_LOCK:
         ws = _WS.get(key)
         if ws is None or ws.numel() < n:
             size = n if ws is None else max(n, 2 * ws.numel())
-            with torch.cuda.device(device):
-                new = torch.zeros(size, dtype=torch.uint8, device=device)
+            new = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", idx))
             if new.data_ptr() % 256:
                 raise RuntimeError("workspace allocation is not 256-byte aligned")
             if ws is not None:
@@ -126,7 +144,32 @@ def _mask_view(mask: torch.Tensor, B: int, cap: int) -> tuple[int, int]:
     return code, (0 if mask.size(0) == 1 else mask.stride(0))
 
 
+_ARGS: dict = {}  # layout of a call (shapes, strides, dtypes, devices, scalars) -> (checked argument bytes, out shape)
+
+
 def _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine):
+    """The bz_gqa_decode_args of a call (pointers of q, k_cache, v_cache and out filled in; ranges, mask and workspace
+    left to the caller) and its output tensor (allocated when out is None). The checks depend only on the tensors'
+    layout, so a layout seen before reuses its checked arguments and only the pointers are set."""
+    key = (q.shape, q.stride(), q.dtype, q.device, k_cache.shape, k_cache.stride(), k_cache.dtype, k_cache.device,
+           v_cache.shape, v_cache.stride(), v_cache.dtype, v_cache.device,
+           None if out is None else (out.shape, out.stride(), out.dtype, out.device),
+           scale, num_splits, max_seq_len, combine)
+    hit = _ARGS.get(key)
+    if hit is None:
+        a, out = _check_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
+        if len(_ARGS) >= 512:
+            _ARGS.clear()
+        _ARGS[key] = (bytes(a), tuple(out.shape))
+        return a, out
+    a = kernels.GqaDecodeArgs.from_buffer_copy(hit[0])
+    if out is None:
+        out = torch.empty(hit[1], dtype=torch.bfloat16, device=q.device)
+    a.q, a.k_cache, a.v_cache, a.out = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr()
+    return a, out
+
+
+def _check_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine):
     _check(q.is_cuda, "query must be a device tensor")
     _check(q.dtype == torch.bfloat16 and k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16,
            "query, k_cache and v_cache must be bf16")
@@ -171,20 +214,23 @@ def _run(a, dev, workspace, entry: str, static_scratch: bool = False) -> None:
     well as under capture). Calls on the scratch must not overlap in time on one device (graph replays or compiled
     calls on several streams). Sizes beyond the scratch (BZ_ERR_SCRATCH) take the stream's cached workspace."""
     lib = kernels.load()
-    with torch.cuda.device(dev):
-        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def launch(stream):
+        sp = ctypes.c_void_p(stream)
         if workspace is None and (static_scratch or torch.cuda.is_current_stream_capturing()):
             if entry == "bz_gqa_decode_masked":
                 a.seq_lens, a.kv_start = None, None  # the noalloc entry takes the range from the mask
-            rc = lib.bz_gqa_decode_noalloc(ctypes.byref(a), stream)
+            rc = lib.bz_gqa_decode_noalloc(ctypes.byref(a), sp)
             if rc != kernels.ERR_SCRATCH:
                 kernels.check(rc, "bz_gqa_decode_noalloc")
                 return
-        ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
-            a.num_splits, a.max_seq_len)
+        ws = workspace if workspace is not None else _stream_workspace(
+            dev.index, stream, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim,
+            a.capacity, a.num_splits, a.max_seq_len)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
-        kernels.check(getattr(lib, entry)(ctypes.byref(a), stream), entry)
+        kernels.check(getattr(lib, entry)(ctypes.byref(a), sp), entry)
+
+    kernels.run_on(dev, launch)
 
 
 def _default_out(q: torch.Tensor) -> torch.Tensor:
@@ -254,10 +300,8 @@ def _gqa_decode_wave(q, k_cache, v_cache, seq_lens, scale, out, kv_start) -> tor
     dev = q.device
     a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
     a.kv_start = _int32_rows(kv_start, a.batch, "kv_start", dev).data_ptr() if kv_start is not None else None
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_gqa_decode_wave(ctypes.byref(a), ctypes.c_void_p(stream)),
-                      "bz_gqa_decode_wave")
+    kernels.run_on(dev, lambda stream: kernels.check(
+        kernels.load().bz_gqa_decode_wave(ctypes.byref(a), ctypes.c_void_p(stream)), "bz_gqa_decode_wave"))
     return out
 
 
@@ -316,10 +360,8 @@ def gqa_decode_probs(q: torch.Tensor, k_cache: torch.Tensor, seq_lens: torch.Ten
     if probs is None:
         probs = torch.empty(a.batch, a.num_q_heads, a.capacity, dtype=torch.float32, device=dev)
     _check_probs(probs, a, dev)
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_gqa_decode_probs(ctypes.byref(a), ctypes.c_void_p(probs.data_ptr()),
-                                                         ctypes.c_void_p(stream)), "bz_gqa_decode_probs")
+    kernels.run_on(dev, lambda stream: kernels.check(kernels.load().bz_gqa_decode_probs(
+        ctypes.byref(a), ctypes.c_void_p(probs.data_ptr()), ctypes.c_void_p(stream)), "bz_gqa_decode_probs"))
     return probs
 
 
@@ -340,11 +382,9 @@ def mask_interval(mask: torch.Tensor, capacity: int, batch: int | None = None,
         kv_start = torch.empty(B, dtype=torch.int32, device=dev)
     _int32_rows(seq_lens, B, "seq_lens", dev)
     _int32_rows(kv_start, B, "kv_start", dev)
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_mask_interval(mask.data_ptr(), code, stride_b, B, int(capacity),
-                                                      seq_lens.data_ptr(), kv_start.data_ptr(),
-                                                      ctypes.c_void_p(stream)), "bz_mask_interval")
+    kernels.run_on(dev, lambda stream: kernels.check(kernels.load().bz_mask_interval(
+        mask.data_ptr(), code, stride_b, B, int(capacity), seq_lens.data_ptr(), kv_start.data_ptr(),
+        ctypes.c_void_p(stream)), "bz_mask_interval"))
     return seq_lens, kv_start
 
 
@@ -412,17 +452,20 @@ def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
     f.q_norm_weight, f.k_norm_weight, f.eps = q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(eps)
     f.cos, f.sin, f.rope_stride_b = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
     f.cache_pos = cache_pos.data_ptr()
-    with torch.cuda.device(dev):
-        ws = workspace if workspace is not None else get_workspace(
-            dev, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim, a.capacity,
-            a.num_splits, a.max_seq_len)
+    if probs is not None:
+        _check_probs(probs, a, dev)
+    lib = kernels.load()
+
+    def launch(stream):
+        ws = workspace if workspace is not None else _stream_workspace(
+            dev.index, stream, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim,
+            a.capacity, a.num_splits, a.max_seq_len)
         f.base.workspace, f.base.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_gqa_decode_fused(ctypes.byref(f), ctypes.c_void_p(stream)),
-                      "bz_gqa_decode_fused")
+        sp = ctypes.c_void_p(stream)
+        kernels.check(lib.bz_gqa_decode_fused(ctypes.byref(f), sp), "bz_gqa_decode_fused")
         if probs is not None:
-            _check_probs(probs, a, dev)
-            kernels.check(kernels.load().bz_gqa_decode_fused_probs(ctypes.byref(f), ctypes.c_void_p(probs.data_ptr()),
-                                                                   ctypes.c_void_p(stream)),
+            kernels.check(lib.bz_gqa_decode_fused_probs(ctypes.byref(f), ctypes.c_void_p(probs.data_ptr()), sp),
                           "bz_gqa_decode_fused_probs")
+
+    kernels.run_on(dev, launch)
     return out

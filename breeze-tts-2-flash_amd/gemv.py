@@ -44,9 +44,8 @@ def _norm_w(nw: torch.Tensor, K: int) -> None:
 
 
 def _launch(a: kernels.GemvArgs, dev: torch.device, what: str) -> None:
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        kernels.check(kernels.load().bz_gemv(ctypes.byref(a), ctypes.c_void_p(stream)), what)
+    kernels.run_on(dev, lambda stream: kernels.check(kernels.load().bz_gemv(ctypes.byref(a), ctypes.c_void_p(stream)),
+                                                     what))
 
 
 def _args(x, y, epilogue) -> kernels.GemvArgs:
@@ -152,8 +151,7 @@ def _rmsnorm(x, w, eps, y) -> torch.Tensor:
     M, K = x.shape
     _norm_w(w, K)
     _y(y, M, K)
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        kernels.check(kernels.load().bz_rmsnorm(x.data_ptr(), x.stride(0), w.data_ptr(), float(eps), y.data_ptr(),
-                                                y.stride(0), M, K, ctypes.c_void_p(stream)), "rmsnorm")
+    kernels.run_on(x.device, lambda stream: kernels.check(kernels.load().bz_rmsnorm(
+        x.data_ptr(), x.stride(0), w.data_ptr(), float(eps), y.data_ptr(), y.stride(0), M, K, ctypes.c_void_p(stream)),
+        "rmsnorm"))
     return y

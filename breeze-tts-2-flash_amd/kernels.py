@@ -219,6 +219,31 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+_TC = None  # torch._C, bound on first use (this module does not import torch at load time)
+
+
+def run_on(device, launch):
+    """launch(stream) with `device` current and `stream` the raw handle of its current stream, as a torch kernel
+    launches: what `with torch.cuda.device(device): launch(torch.cuda.current_stream(device).cuda_stream)` does,
+    without building a stream object and switching the device only when another one is current (several us less host
+    time per call). Returns what launch returns."""
+    global _TC
+    tc = _TC
+    if tc is None:
+        import torch
+
+        tc = _TC = torch._C
+    prev = tc._cuda_getDevice()
+    idx = prev if device.index is None else device.index
+    if prev == idx:
+        return launch(tc._cuda_getCurrentRawStream(idx))
+    tc._cuda_setDevice(idx)
+    try:
+        return launch(tc._cuda_getCurrentRawStream(idx))
+    finally:
+        tc._cuda_setDevice(prev)
+
+
 _DEVICE_REASON: dict = {}
 
 

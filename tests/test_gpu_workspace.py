@@ -97,7 +97,7 @@ def test_cached_workspace_stays_bounded(device):
     torch.cuda.synchronize()
     grown = len(attention._WS) + len(attention._WS_RETIRED) - before
     assert grown <= 8, f"{grown} workspaces allocated over 163 growing lengths"
-    ws = attention._WS[(str(device), torch.cuda.current_stream(device).cuda_stream, B * NKV)]
+    ws = attention._WS[(device.index, torch.cuda.current_stream(device).cuda_stream, B * NKV)]
     _counters_clear(ws, B * NKV, "cached workspace")
 
 
