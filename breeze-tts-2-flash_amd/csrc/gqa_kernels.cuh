@@ -289,36 +289,74 @@ __device__ void merge_splits(const Params& p, int z, int h, int nact) {
   }
 }
 
+// Blocks of positions with at least one attended position, recorded while a mask row is scanned: bit i of the
+// kValidWords words covers positions [i << shift, (i + 1) << shift), shift >= 6 chosen so that the capacity fits.
+constexpr int kValidWords = 64;
+__device__ __forceinline__ int valid_shift(int cap) {
+  int s = 6;
+  while (((cap - 1) >> s) >= 32 * kValidWords) ++s;
+  return s;
+}
+// Whether [lo, hi) holds a block with an attended position (uniform over the workgroup: every thread reads the same
+// LDS words).
+__device__ __forceinline__ bool any_valid(const uint32_t* bits, int shift, int lo, int hi) {
+  if (hi <= lo) return false;
+  for (int blk = lo >> shift; blk <= (hi - 1) >> shift; ++blk)
+    if (bits[blk >> 5] & (1u << (blk & 31))) return true;
+  return false;
+}
+
 // [start, end) of mask row b: the first and last position below capacity whose mask value is > -1e30, or [0, 0) if
 // there is none (what mask_range_kernel computes, and bz_mask_interval returns). All NT threads of the workgroup
-// take part, and all get the result.
-template <int NT>
-__device__ void mask_row_range(const Params& p, int b, int& start, int& end) {
+// take part, and all get the result. With bits (kValidWords words of LDS), the blocks holding attended positions are
+// recorded there too (valid_shift(cap)), so a workgroup can skip a chunk the mask excludes entirely, as the
+// reference skips its fully masked 64-position chunks (bb_attn.cu:9-11, :151-154).
+template <int NT, int MK>
+__device__ void mask_row_range_t(const Params& p, int b, int& start, int& end, uint32_t* bits) {
+  constexpr int kUnroll = 8;  // mask values per thread loaded before any is compared: one round trip per 8 NT
   __shared__ int s_lo[NT / kWave], s_hi[NT / kWave];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int shift = valid_shift(p.cap);
+  if (bits != nullptr) {
+    for (int i = tid; i < kValidWords; i += NT) bits[i] = 0;
+    __syncthreads();
+  }
+  // the row through a buffer resource cut at the capacity: every load is unconditional (loads past it read 0 and
+  // touch no memory), so the compiler issues the kUnroll loads together
+  constexpr int kBytes = MK == BZ_MASK_BF16 ? 2 : 4;
+  const Rsrc rm = span_rsrc(static_cast<const char*>(p.mask) + (int64_t)b * p.m_sb * kBytes, p.cap * kBytes);
   int lo = p.cap, hi = -1;
-  const int64_t row = (int64_t)b * p.m_sb;
-  if (p.mask_kind == BZ_MASK_BF16) {
-    for (int pos = tid; pos < p.cap; pos += NT)
-      if (bf16_to_f32(static_cast<const uint16_t*>(p.mask)[row + pos]) > kExcluded) {
+  for (int base = 0; base < p.cap; base += kUnroll * NT) {
+    float m[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t off = (uint32_t)(base + u * NT + tid) * kBytes;
+      m[u] = MK == BZ_MASK_BF16 ? bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rm, off, 0, 0))
+                                : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, off, 0, 0));
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int pos = base + u * NT + tid;
+      const bool keep = pos < p.cap && m[u] > kExcluded;
+      if (keep) {
         lo = min(lo, pos);
         hi = max(hi, pos);
       }
-  } else {
-    for (int pos = tid; pos < p.cap; pos += NT)
-      if (static_cast<const float*>(p.mask)[row + pos] > kExcluded) {
-        lo = min(lo, pos);
-        hi = max(hi, pos);
+      // a wave's 64 positions here are one aligned run of 64, inside one block (shift >= 6): one LDS OR per wave
+      if (bits != nullptr && __ballot(keep) != 0 && lane == 0) {
+        const int blk = (base + u * NT + wave * kWave) >> shift;
+        atomicOr(&bits[blk >> 5], 1u << (blk & 31));
       }
+    }
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
     lo = min(lo, __shfl_xor(lo, off));
     hi = max(hi, __shfl_xor(hi, off));
   }
-  if (tid % kWave == 0) {
-    s_lo[tid / kWave] = lo;
-    s_hi[tid / kWave] = hi;
+  if (lane == 0) {
+    s_lo[wave] = lo;
+    s_hi[wave] = hi;
   }
   __syncthreads();
   lo = s_lo[0];
@@ -332,14 +370,24 @@ __device__ void mask_row_range(const Params& p, int b, int& start, int& end) {
   end = hi >= 0 ? hi + 1 : 0;
 }
 
+// MK: the mask's dtype when the caller is built for one, BZ_MASK_NONE to take it from p.mask_kind.
+template <int NT, int MK = BZ_MASK_NONE>
+__device__ __forceinline__ void mask_row_range(const Params& p, int b, int& start, int& end, uint32_t* bits = nullptr) {
+  if (MK == BZ_MASK_BF16 || (MK == BZ_MASK_NONE && p.mask_kind == BZ_MASK_BF16))
+    mask_row_range_t<NT, BZ_MASK_BF16>(p, b, start, end, bits);
+  else
+    mask_row_range_t<NT, BZ_MASK_F32>(p, b, start, end, bits);
+}
+
 // Range of query token t of row b, from seq_lens / kv_start or, when seq_lens is NULL, from the mask row (all NT
-// threads of the workgroup must call it then).
-template <int NT>
-__device__ __forceinline__ void unit_range(const Params& p, int b, int t, int& start, int& end) {
+// threads of the workgroup must call it then; bits as in mask_row_range).
+template <int NT, int MK = BZ_MASK_NONE>
+__device__ __forceinline__ void unit_range(const Params& p, int b, int t, int& start, int& end,
+                                           uint32_t* bits = nullptr) {
   if (p.seq_lens != nullptr) {
     row_range(p, b, start, end);
   } else {
-    mask_row_range<NT>(p, b, start, end);
+    mask_row_range<NT, MK>(p, b, start, end, bits);
   }
   end = max(start, end - (p.T - 1 - t));
 }
@@ -504,13 +552,20 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   }
 
   int start, end;
-  unit_range<NT>(p, b, tok, start, end);
+  __shared__ uint32_t s_valid[MK != BZ_MASK_NONE ? kValidWords : 1];
+  unit_range<NT, MK>(p, b, tok, start, end, MK != BZ_MASK_NONE ? s_valid : nullptr);
   const int len = end - start;
   const int chunk = split_chunk<D>(len, p.splits, p.min_chunk);
   const int nact = split_count(len, chunk);
   if (split >= nact) return;
   const int lo = start + split * chunk;
-  const int hi = min(lo + chunk, end);
+  const int hi_chunk = min(lo + chunk, end);
+  // A chunk whose every position the mask excludes streams nothing (its partial is empty: max -inf, sum 0); the
+  // scan of the mask row recorded which blocks of positions hold an attended one. hi_chunk still decides which
+  // workgroup owns the fused step's cache slot.
+  const bool skip = MK != BZ_MASK_NONE && p.seq_lens == nullptr &&
+                    !any_valid(s_valid, valid_shift(p.cap), lo, hi_chunk);
+  const int hi = skip ? lo : hi_chunk;
 
   Spans sp;
   {
@@ -554,7 +609,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
       // one writer per (row, kv head): the workgroup whose chunk holds the slot, or split 0 when the slot lies
       // outside the row's attended range; only that workgroup can read the slot in this call, from registers
       const bool in_range = pos >= start && pos < end;
-      const bool owner = in_range ? (pos >= lo && pos < hi) : (split == 0);
+      const bool owner = in_range ? (pos >= lo && pos < hi_chunk) : (split == 0);
       if (owner) {
         if (in_range) newpos = pos;
         if (tid < LPR) {
@@ -758,7 +813,7 @@ __global__ void __launch_bounds__(kThreads) gqa_probs_kernel(const Params p, flo
     qh = s_q;
   }
   int start, end;
-  unit_range<kThreads>(p, b, 0, start, end);
+  unit_range<kThreads, MK>(p, b, 0, start, end);
   float* const row = probs + ((int64_t)b * p.NH + hq) * p.cap;
   const uint16_t* const kb = p.k + (int64_t)b * p.kv_sb + (int64_t)h * p.kv_sh;
   float mx = -INFINITY;
