@@ -3,15 +3,17 @@
 Each case draws batch 1..6, kv heads 1/2/4/8, group 1/2/4/8, head_dim 64/128, a capacity of 1..600 slots, per-row
 lengths 0..capacity and starts 0..length (empty and one-position rows included), 1 or 2 query tokens per row, a split
 count (0 = default, 1, 3, 8, 17), a merge mode and, in about a third of the cases, an additive mask (bf16 or fp32,
-values in [-2, 2] with excluded holes inside the range), with the K/V cache positions outside each row's range set to
-NaN. It runs bz_gqa_decode with the drawn options and, without a mask, bz_gqa_decode_wave. Tolerance
+values in [-2, 2] with excluded holes inside the range, in half of those also runs of 32..200 excluded positions), with
+the K/V cache positions outside each row's range set to NaN. It runs bz_gqa_decode with the drawn options and, without
+a mask, bz_gqa_decode_wave; with a mask and one query token also bz_gqa_decode_masked, whose range comes from the mask
+(then also excluding what lies outside the row's range), so that chunks the mask excludes entirely are skipped. Tolerance
 |out - ref| <= 2e-3 + 1e-2 |ref| (the north star's), every output finite, rows with nothing to attend exactly 0.
 """
 import numpy as np
 import pytest
 import torch
 
-from breeze_tts_2_flash_amd import gqa_decode, gqa_decode_wave
+from breeze_tts_2_flash_amd import gqa_decode, gqa_decode_masked, gqa_decode_wave
 from oracle.attention import decode_attention_tokens
 from oracle.bf16 import f32_to_bf16
 
@@ -43,7 +45,13 @@ def draw(seed):
     mask = None
     if rng.random() < 0.35:
         mask = rng.uniform(-2.0, 2.0, size=(B, cap)).astype(np.float32)
-        mask[rng.random((B, cap)) < 0.1] = -np.inf if rng.random() < 0.5 else np.finfo(np.float32).min
+        excl = -np.inf if rng.random() < 0.5 else np.finfo(np.float32).min
+        mask[rng.random((B, cap)) < 0.1] = excl
+        if rng.random() < 0.5:  # runs of 32..200 excluded positions: whole chunks the masked entry skips
+            for b in range(B):
+                for _ in range(int(rng.integers(1, 4))):
+                    lo = int(rng.integers(0, cap))
+                    mask[b, lo:lo + int(rng.integers(32, 201))] = excl
     mask_dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
     return dict(B=B, NKV=NKV, G=G, D=D, cap=cap, T=T, lens=lens.astype(np.int32), starts=starts.astype(np.int32),
                 splits=splits, combine=combine, q=q, k=k, v=v, mask=mask, mask_dtype=mask_dtype)
@@ -74,6 +82,15 @@ def test_random_case(device, seed):
                                      combine=c["combine"])}
     if mask is None:
         outs["gqa_decode_wave"] = gqa_decode_wave(q, k, v, lens, scale, kv_start=starts)
+    elif c["T"] == 1:
+        # the masked entry takes the range from the mask: exclude what lies outside [start, end) as well
+        inside = np.zeros_like(c["mask"], dtype=bool)
+        for b in range(c["B"]):
+            inside[b, c["starts"][b]:c["lens"][b]] = True
+        full = np.where(inside, c["mask"], np.float32(-np.inf))
+        mfull = torch.from_numpy(full).to(c["mask_dtype"]).to(device)[:, None, None, :]
+        outs["gqa_decode_masked"] = gqa_decode_masked(q, k, v, mfull, scale, num_splits=c["splits"],
+                                                      combine=c["combine"])
     torch.cuda.synchronize()
     for name, out in outs.items():
         got = out.float().cpu().numpy().reshape(ref.shape)
