@@ -271,6 +271,25 @@ def test_wave_validation(lib, K, over, code):
     assert lib.bz_gqa_decode_wave(None, None) == -1
 
 
+@pytest.mark.parametrize("over,probs,code", [
+    (dict(), None, -1),                                        # no output buffer
+    (dict(seq_lens=None), 0x80000, -1),                        # neither seq_lens nor a mask
+    (dict(tokens_per_row=2, q_stride_t=128), 0x80000, -3),     # one query token per row
+    (dict(), 0x80002, -4),                                     # probs not 4-byte aligned
+    (dict(mask=0x50000, mask_dtype=0), 0x80000, -6),           # mask without a dtype
+    (dict(head_dim=96), 0x80000, -3),
+    (dict(q=None), 0x80000, -1),
+])
+def test_probs_validation(lib, K, over, probs, code):
+    a = _good_args(K, **over)
+    assert lib.bz_gqa_decode_probs(ctypes.byref(a), probs, None) == code
+    assert lib.bz_gqa_decode_probs(None, 0x80000, None) == -1
+    f = _good_fused(K, **{"base_" + k: v for k, v in over.items() if k != "q"})
+    if "q" not in over and "head_dim" not in over and "tokens_per_row" not in over:
+        assert lib.bz_gqa_decode_fused_probs(ctypes.byref(f), probs, None) == code
+    assert lib.bz_gqa_decode_fused_probs(None, 0x80000, None) == -1
+
+
 def test_mask_interval_validation(lib, K):
     f = lib.bz_mask_interval
     ok = (0x50000, K.MASK_BF16, 2048, 2, 2048, 0x60000, 0x60010, None)
