@@ -227,30 +227,36 @@ __device__ void merge_splits(const Params& p, int z, int h, int nact) {
   const int b = z / p.T, tok = z - b * p.T;
   uint16_t* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)tok * p.o_st;
 
+  // The (max, sum) pairs of q head wave % G first, by every wave and without a condition (a wave past the group's
+  // heads works a head out again and stores nothing): loads complete in issue order, so the split weights are
+  // worked out while the accumulators are still on their way.
+  using Pair = decltype(__builtin_amdgcn_raw_buffer_load_b64(rml, 0, 0, kSc1));
+  Pair raw[kPerLane];
+  auto load_ml = [&](int g) {
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      raw[j] = __builtin_amdgcn_raw_buffer_load_b64(rml, ((lane + kWave * j) * G + g) * 8, 0, kSc1);
+  };
+  load_ml(wave % G);
+  // the accumulators, also unconditionally: threads past the group's G * D values (G * D < NT) load one of them
+  // again and drop it, so that the compiler's count of loads in flight stays exact
   float t[kOut][kBatch];
 #pragma unroll
   for (int k = 0; k < kOut; ++k) {
-    const int o = tid + k * NT;
-    if (o < GD) {  // uniform over the wave: GD is a multiple of 64
+    const int o = (tid + k * NT) % GD;
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        t[k][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(racc, (u * GD + o) * 4, 0, kSc1));
-    }
+    for (int u = 0; u < kBatch; ++u)
+      t[k][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(racc, (u * GD + o) * 4, 0, kSc1));
   }
-  float mv[kPerLane], lv[kPerLane];
-  auto load_ml = [&](int g) {
+
+  // split weights w_s = 2^(m_s - M) / sum_s 2^(m_s - M) l_s of head g, from the pairs in raw
+  auto weights = [&](int g) {
+    float mv[kPerLane], lv[kPerLane];
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
-      const int sp = lane + kWave * j;
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rml, (sp * G + g) * 8, 0, kSc1);
-      mv[j] = sp < nact ? __uint_as_float(v[0]) : -INFINITY;
-      lv[j] = __uint_as_float(v[1]);  // 0 past nact
+      mv[j] = lane + kWave * j < nact ? __uint_as_float(raw[j][0]) : -INFINITY;
+      lv[j] = __uint_as_float(raw[j][1]);  // 0 past nact
     }
-  };
-  if (wave < G) load_ml(wave);
-
-  for (int g = wave; g < G; g += NW) {
-    if (g != wave) load_ml(g);
     float mloc = mv[0];
 #pragma unroll
     for (int j = 1; j < kPerLane; ++j) mloc = fmaxf(mloc, mv[j]);
@@ -264,8 +270,15 @@ __device__ void merge_splits(const Params& p, int z, int h, int nact) {
     }
     const float L = wave_sum(lloc);
     const float inv = L > 0.f ? 1.f / L : 0.f;
+    if (wave < G) {  // waves past the group's heads only followed along
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j) s_w[g][lane + kWave * j] = mv[j] * inv;
+      for (int j = 0; j < kPerLane; ++j) s_w[g][lane + kWave * j] = mv[j] * inv;
+    }
+  };
+  weights(wave % G);
+  for (int g = wave + NW; g < G; g += NW) {  // groups of more q heads than waves
+    load_ml(g);
+    weights(g);
   }
   __syncthreads();
 
