@@ -442,41 +442,41 @@ __device__ __forceinline__ void load_tile(Tile<PPT>& t, const Spans& sp, int pos
 // Fold one tile into the running (max m, sum l, acc) per q head: q.k as four bf16 dot2 per head plus a DPP row sum,
 // scaled by scale * log2(e); online softmax in base 2 with one max per wave (m is wave-uniform, l and acc per row);
 // then P.V in fp32 on the unpacked V registers.
-// A slot whose row lies past hi (or, with LO, before lo) is skipped (the condition is uniform over the row's lanes, so
-// the DPP sum, which reads only lanes of the same row, never sees a skipped lane).
+// A slot whose row lies past hi (or, with LO, before lo) is dropped (the condition is uniform over the row's lanes, and
+// the DPP sum reads only lanes of the same row, so whatever the dropped slot holds stays in its own row).
 // Fused prologue: the slot newpos (>= 0 only in the workgroup whose chunk holds it) takes the new k / v computed in
 // registers; the cache write of this call is not read back.
 template <int LPR, int ROWS, int G, int PPT, int MK, bool FUSED, bool LO = false>
 __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G], float scale_log2, float (&m)[G],
                                              float (&l)[G], float (&acc)[G][8], int pos0, int hi, int newpos,
                                              const uint4& knew, const uint4& vnew, int lo = 0) {
+  // No branch: every slot's products are computed and a slot outside the range (or excluded by the mask) is dropped
+  // by selects, its score to -inf and its V to 0 (so NaN there reaches neither the sums nor the accumulator through
+  // 0 * V). Branches here would also make the compiler's waits for the tile's loads conservative.
+  auto sel = [](bool c, const uint4& a, const uint4& b) {
+    return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+  };
   float s[G][PPT];
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) s[g][i] = -INFINITY;
     const int pos = pos0 + ROWS * i;
-    if (pos < hi && (!LO || pos >= lo)) {
-      if (FUSED && pos == newpos) {
-        t.k[i] = knew;
-        t.v[i] = vnew;
-      }
-      bool inc = true;
-      if (MK != BZ_MASK_NONE) {
-        inc = t.m[i] > kExcluded;
-        // an excluded position must not touch the accumulator even through 0 * V (V may hold NaN there)
-        if (!inc) t.v[i] = make_uint4(0, 0, 0, 0);
-      }
+    bool inc = pos < hi && (!LO || pos >= lo);
+    if (FUSED) {
+      const bool fresh = pos == newpos;
+      t.k[i] = sel(fresh, knew, t.k[i]);
+      t.v[i] = sel(fresh, vnew, t.v[i]);
+    }
+    if (MK != BZ_MASK_NONE) inc = inc && t.m[i] > kExcluded;
+    t.v[i] = sel(inc, t.v[i], make_uint4(0, 0, 0, 0));
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = dot2_bf16(qp[g].x, t.k[i].x, 0.f);
-        d = dot2_bf16(qp[g].y, t.k[i].y, d);
-        d = dot2_bf16(qp[g].z, t.k[i].z, d);
-        d = dot2_bf16(qp[g].w, t.k[i].w, d);
-        d = row_sum<LPR>(d) * scale_log2;
-        if (MK != BZ_MASK_NONE) d = fmaf(t.m[i], kLog2e, d);
-        if (inc) s[g][i] = d;
-      }
+    for (int g = 0; g < G; ++g) {
+      float d = dot2_bf16(qp[g].x, t.k[i].x, 0.f);
+      d = dot2_bf16(qp[g].y, t.k[i].y, d);
+      d = dot2_bf16(qp[g].z, t.k[i].z, d);
+      d = dot2_bf16(qp[g].w, t.k[i].w, d);
+      d = row_sum<LPR>(d) * scale_log2;
+      if (MK != BZ_MASK_NONE) d = fmaf(t.m[i], kLog2e, d);
+      s[g][i] = inc ? d : -INFINITY;
     }
   }
   // one running max per wave: the rows of a wave can then be merged by plain sums
@@ -506,14 +506,12 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
   }
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-    if (pos0 + ROWS * i < hi && (!LO || pos0 + ROWS * i >= lo)) {
-      float vf[8];
-      unpack8(t.v[i], vf);
+    float vf[8];
+    unpack8(t.v[i], vf);
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
-    }
+      for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(s[g][i], vf[j], acc[g][j]);
   }
 }
 
