@@ -95,13 +95,15 @@ FLUSH_BYTES = 1 << 30       # untimed write right before each timed replay
 EXTRA_CALLS = 1000          # timed calls of each extra workload, whatever --steps is
 EXTRA_FRAMES = 200          # timed depth frames
 BACKBONE_REPS = 100         # timed backbone steps (and replays of each GEMV's 28-layer graph)
+BACKBONE_CHAIN = 5          # steps per replay for the back-to-back backbone figure
 
 _FLUSH = {}
 
 
 def flush_caches(dev):
     """Write FLUSH_BYTES on the current stream: evicts the L2s and the MALL (more than four times their size), and
-    keeps the GPU busy for ~150 µs while the host goes on to submit what follows."""
+    keeps the GPU busy for ~150 µs while the host goes on to submit what follows. (A read of another FLUSH_BYTES after
+    the write, so that the caches hold clean lines, measured the same.)"""
     import torch
 
     buf = _FLUSH.get(dev)
@@ -252,12 +254,9 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=F
 BACKBONE = dict(H=2048, nq=2048, nk=1024, inter=6144, layers=28, D=128, cap=2048, len=1024)
 
 
-def time_backbone(pkg, dev, reps=BACKBONE_REPS):
-    """The reference's backbone decode step at its serving shape (a Qwen3 of hidden 2048, 16 q / 8 KV heads of 128,
-    intermediate 6144, 28 layers; the CFG pair, M = 2; KV 1024 of 2048 slots) on random-init weights: per layer
-    gemv_seg (RMSNorm + q|k|v) -> gqa_decode_fused -> gemv_resid (o_proj) -> gemv_gateup -> gemv_resid (down), then
-    the final rmsnorm (flash/backbone.py:120-129), one HIP graph per step. Also each GEMV alone, rotating over the 28
-    layers' weights. Returns {name: {us, bytes, GB/s}}."""
+def make_backbone(dev):
+    """Random-init weights, KV caches and buffers of the reference's backbone at its serving shape (a Qwen3 of hidden
+    2048, 16 q / 8 KV heads of 128, intermediate 6144, 28 layers; the CFG pair, M = 2; KV 1024 of 2048 slots)."""
     import torch
 
     c = BACKBONE
@@ -292,6 +291,24 @@ def time_backbone(pkg, dev, reps=BACKBONE_REPS):
     sin = ang.sin().to(bf).expand(M, D).contiguous().to(dev)
     cache_pos = torch.tensor([pos], dtype=torch.int64, device=dev)
     lens = torch.full((M,), c["len"], dtype=torch.int32, device=dev)
+    return dict(layers=layers, norm_w=norm_w, x0=x0, qkv=qkv, ao=ao, h1=h1, act=act, xb=xb, hidden=hidden, cos=cos,
+                sin=sin, cache_pos=cache_pos, lens=lens)
+
+
+def time_backbone(pkg, dev, reps=BACKBONE_REPS, model=None):
+    """The backbone decode step of make_backbone (or `model`, made earlier by it): per layer gemv_seg (RMSNorm +
+    q|k|v) -> gqa_decode_fused -> gemv_resid (o_proj) -> gemv_gateup -> gemv_resid (down), then the final rmsnorm
+    (flash/backbone.py:120-129), one HIP graph per step. Also each GEMV alone, rotating over the 28 layers' weights.
+    Returns {name: {us, bytes, GB/s}}."""
+    import torch
+
+    c = BACKBONE
+    H, nq, nk, I, L, D = c["H"], c["nq"], c["nk"], c["inter"], c["layers"], c["D"]
+    M = 2
+    m = model if model is not None else make_backbone(dev)
+    layers, norm_w, x0, qkv, ao, h1, act, xb, hidden = (m[k] for k in ("layers", "norm_w", "x0", "qkv", "ao", "h1",
+                                                                         "act", "xb", "hidden"))
+    cos, sin, cache_pos, lens = m["cos"], m["sin"], m["cache_pos"], m["lens"]
     eps, scale = 1e-6, D ** -0.5
 
     def step():
@@ -306,19 +323,27 @@ def time_backbone(pkg, dev, reps=BACKBONE_REPS):
             x = xb[i % 2]
         pkg.rmsnorm(x, norm_w, eps, hidden)
 
-    def graph_time(fn, reps):
-        """Median µs of `reps` replays of fn captured in one graph, each replay timed alone after a cache flush."""
+    def graph_time(fn, reps, flush=True):
+        """Median µs of `reps` replays of fn captured in one graph, each replay timed alone (after a cache flush)."""
         fn()
         torch.cuda.synchronize()
         timed = capture_timed(fn, dev)
-        return statistics.median(time_captured(timed, dev) for _ in range(reps))
+        return statistics.median(time_captured(timed, dev, flush=flush) for _ in range(reps))
 
     out = {}
     layer_bytes = 2 * ((nq + 2 * nk) * H + H * nq + 2 * I * H + H * I) + 2 * 2 * (nk // D) * c["len"] * D * M
-    us = graph_time(step, reps)
-    out["backbone_step_28_layers"] = {"us": round(us, 1), "bytes": L * layer_bytes,
-                                      "GB/s": round(L * layer_bytes / us / 1e3, 1),
-                                      "pct_of_peak_hbm": round(100.0 * L * layer_bytes / us / 1e3 / PEAK_HBM_GBS, 1)}
+
+    def entry(us):
+        return {"us": round(us, 1), "bytes": L * layer_bytes, "GB/s": round(L * layer_bytes / us / 1e3, 1),
+                "pct_of_peak_hbm": round(100.0 * L * layer_bytes / us / 1e3 / PEAK_HBM_GBS, 1)}
+    out["backbone_step_28_layers"] = entry(graph_time(step, reps))
+    # steps back to back and no flush, as a serving loop runs them: the caches hold what the previous steps left
+    chain = BACKBONE_CHAIN
+
+    def steps():
+        for _ in range(chain):
+            step()
+    out["backbone_step_28_layers_back_to_back"] = entry(graph_time(steps, max(3, reps // 10), flush=False) / chain)
     # each GEMV alone, over the 28 layers' weights in turn (28 launches per replay)
     cases = {
         "gemv_qkv_norm": (lambda ly: pkg.gemv_seg(x0, ly["ln1"], eps, ly["wq"], ly["wk"], ly["wv"], qkv),
@@ -332,7 +357,6 @@ def time_backbone(pkg, dev, reps=BACKBONE_REPS):
         us = graph_time(lambda: [fn(ly) for ly in layers], reps) / L
         out[name] = {"us": round(us, 3), "weight_bytes": wbytes, "GB/s": round(wbytes / us / 1e3, 1),
                      "pct_of_peak_hbm": round(100.0 * wbytes / us / 1e3 / PEAK_HBM_GBS, 1)}
-    del layers
     return out
 
 
@@ -626,7 +650,8 @@ def main():
         print(f"[bench] real depth shape frame: {us_r:.3f} us/frame ({us_rs:.3f} with the split kernel)",
               file=sys.stderr, flush=True)
         bb = time_backbone(pkg, dev)
-        bb["timing"] = f"median of {BACKBONE_REPS} graph replays, each after a {FLUSH_BYTES >> 20} MiB cache flush"
+        bb["timing"] = (f"median of {BACKBONE_REPS} graph replays, each after a {FLUSH_BYTES >> 20} MiB cache flush; "
+                        f"back_to_back: {BACKBONE_CHAIN} steps per replay, no flush, median of {max(3, BACKBONE_REPS // 10)}")
         extra["backbone"] = bb
         for k, v in bb.items():
             print(f"[bench] {k}: {v}", file=sys.stderr, flush=True)
