@@ -298,6 +298,8 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   const int NH = a->num_q_heads, NKV = a->num_kv_heads, D = a->head_dim, cap = a->capacity;
   const int G = NH / NKV, R = rows_of(a);
   if (a->combine < BZ_COMBINE_AUTO || a->combine > BZ_COMBINE_KERNEL) return BZ_ERR_COMBINE_MODE;
+  // the split kernels built without a mask take each row's range from seq_lens alone
+  if (mask_kind == BZ_MASK_NONE && seq_lens == nullptr) return BZ_ERR_NULL;
   if (seq_lens != nullptr && wave_route(a, mask_kind, f)) return launch_wave(a, stream, seq_lens, kv_start);
   int splits = 0;
   int rc = resolve_splits(a, &splits);
