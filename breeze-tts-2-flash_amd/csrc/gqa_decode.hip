@@ -191,6 +191,7 @@ Params base_params(const bz_gqa_decode_args* a, const int32_t* seq_lens, const i
   p.G = a->num_q_heads / a->num_kv_heads;
   p.cap = a->capacity;
   p.splits = 1;
+  p.inv_splits = 1.0f;
   return p;
 }
 
@@ -342,6 +343,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
 
   Params p = base_params(a, seq_lens, kv_start);
   p.splits = splits;
+  p.inv_splits = 1.0f / (float)splits;
   p.min_chunk = min_chunk;
   p.mask_kind = mask_kind;
   p.combine_last = two_kernels ? 0 : 1;

@@ -51,6 +51,7 @@ struct Params {
   uint16_t* out;
   int64_t o_sb, o_sh, o_st;
   int B, NH, NKV, cap, splits, min_chunk;
+  float inv_splits;  // 1 / splits rounded to float (split_chunk's quotient estimate)
   int G;             // NH / NKV
   int mask_kind;     // bz_mask_dtype of mask (for the merge kernel, which is not templated on it)
   int combine_last;  // 1: last workgroup of each (b, kv head) merges the splits
@@ -181,10 +182,22 @@ constexpr int one_split_len() { return kOneSplitBytes / (4 * D); }
 
 // Positions per split and number of non-empty splits for a row of length len (>= 1 split even when empty, so
 // that someone writes the row's output).
+// ceil(n / d) for 0 <= n < 2^24 without an integer division (about 30 dependent instructions): inv_d is 1 / d within
+// one ulp (rounded, or v_rcp_f32), and d >= 2 or inv_d exactly 1, so the float quotient is within one of floor(n / d)
+// and one correction step makes it exact (checked on the CPU against integer division for d up to 4096 with both
+// neighbours of the rounded 1 / d)
+__device__ __forceinline__ int ceil_div_est(int n, int d, float inv_d) {
+  int q = (int)((float)n * inv_d);
+  int r = n - q * d;
+  q = r < 0 ? q - 1 : (r >= d ? q + 1 : q);
+  r = n - q * d;
+  return q + (r > 0);
+}
+
 template <int D>
-__device__ __forceinline__ int split_chunk(int len, int splits, int min_chunk) {
+__device__ __forceinline__ int split_chunk(int len, int splits, float inv_splits, int min_chunk) {
   if (len <= one_split_len<D>()) return len > min_chunk ? len : min_chunk;
-  const int c = (len + splits - 1) / splits;
+  const int c = ceil_div_est(len, splits, inv_splits);
   return c > min_chunk ? c : min_chunk;
 }
 __device__ __forceinline__ int split_count(int len, int chunk) { return len > 0 ? (len + chunk - 1) / chunk : 1; }
@@ -527,7 +540,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
 
   const int split = blockIdx.x, h = blockIdx.y, z = blockIdx.z;  // z = row * T + token
-  const int b = z / p.T, tok = z - b * p.T;
+  const int b = p.T == 1 ? z : z / p.T, tok = z - b * p.T;  // T = 1 but in the depth step's two-token first step
   const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
 
   // q of the G heads of this group, this lane's 8 dims, issued first, since none of it depends on the row's length.
@@ -573,9 +586,8 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     unit_range<NT, MK>(p, b, tok, start, end, s_valid);
   }
   const int len = end - start;
-  const int chunk = split_chunk<D>(len, p.splits, p.min_chunk);
-  const int nact = split_count(len, chunk);
-  if (split >= nact) return;
+  const int chunk = split_chunk<D>(len, p.splits, p.inv_splits, p.min_chunk);
+  if (split > 0 && split * chunk >= len) return;  // past the row's last non-empty chunk (split 0 always stays)
   const int lo = start + split * chunk;
   const int hi_chunk = min(lo + chunk, end);
   // A chunk whose every position the mask excludes streams nothing (its partial is empty: max -inf, sum 0); the
@@ -607,6 +619,9 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   // keep the machine scheduler from sinking the tile loads below the q / prologue arithmetic (which would make that
   // arithmetic wait for its own inputs before any K/V load is in flight)
   __builtin_amdgcn_sched_barrier(0);
+  // non-empty chunks of the row (1 for an empty row); without a branch, which would make the compiler wait for the
+  // tiles before the q / prologue arithmetic below (chunk >= min_chunk >= 32)
+  const int nact = ceil_div_est(max(len, 1), chunk, __builtin_amdgcn_rcpf((float)chunk));
 
   uint4 qp[G], knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
   int newpos = -1;
@@ -751,7 +766,7 @@ __global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
   int start, end;
   unit_range<kThreads>(p, z / p.T, z % p.T, start, end);
   const int len = end - start;
-  const int nact = split_count(len, split_chunk<D>(len, p.splits, p.min_chunk));
+  const int nact = split_count(len, split_chunk<D>(len, p.splits, p.inv_splits, p.min_chunk));
   if (nact == 1) return;  // the split kernel wrote the output
   merge_splits<D, G, kThreads>(p, z, h, nact);
 }
