@@ -263,14 +263,18 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=F
 
 BACKBONE = dict(H=2048, nq=2048, nk=1024, inter=6144, layers=28, D=128, cap=2048, len=1024)
 STREAM_WGS = (256, 512, 1024)
+# weight bytes of the backbone's GEMVs (bf16, hidden 2048, 16 q / 8 KV heads of 128, intermediate 6144)
+BACKBONE_GEMV_BYTES = {"gemv_qkv_norm_bytes": 2 * 4096 * 2048, "gemv_o_resid_bytes": 2 * 2048 * 2048,
+                       "gemv_gateup_norm_silu_bytes": 2 * 2 * 6144 * 2048, "gemv_down_resid_bytes": 2 * 2048 * 6144}
 
 
-def time_stream_floor(dev, call_bytes):
-    """The floor that one launch and the memory system set for reading call_bytes: µs per launch of a pure streaming
-    read (libbz_bench_stamp.so's bz_bench_stream_read: 256 threads per workgroup, eight 16-byte non-temporal loads
-    per thread in flight, nothing done with the bytes) timed exactly as the cold attention calls are (EXTRA_CALLS
-    launches in one HIP graph between GPU stamps, 2 untimed lead launches, rotating over ROTATE_BYTES, after a flush),
-    on 256, 512 and 1024 workgroups. Returns ({workgroups: µs per launch}, bytes read per launch)."""
+def time_stream_floor(dev, sizes):
+    """The floor that one launch and the memory system set for reading a given number of bytes: µs per launch of a
+    pure streaming read (libbz_bench_stamp.so's bz_bench_stream_read: 256 threads per workgroup, eight 16-byte
+    non-temporal loads per thread in flight, nothing done with the bytes) timed exactly as the cold attention calls
+    are (EXTRA_CALLS launches in one HIP graph between GPU stamps, 2 untimed lead launches, rotating over ROTATE_BYTES,
+    after a flush), on 256, 512 and 1024 workgroups. sizes: {name: bytes per launch}. Returns
+    {name: ({workgroups: µs per launch}, bytes read per launch)}."""
     import ctypes
 
     import torch
@@ -278,32 +282,35 @@ def time_stream_floor(dev, call_bytes):
     lib = GpuStamps.library()
     buf = torch.empty(int(ROTATE_BYTES), dtype=torch.uint8, device=dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    res = {}
-    nbytes = call_bytes
-    for wgs in STREAM_WGS:
-        per_wg = call_bytes // wgs // 16 * 16
-        nbytes = per_wg * wgs
-        regions = buf.numel() // nbytes
-        assert regions > EXTRA_CALLS // 4
+    out = {}
+    for name, call_bytes in sizes.items():
+        res = {}
+        nbytes = call_bytes
+        for wgs in STREAM_WGS:
+            per_wg = call_bytes // wgs // 16 * 16
+            nbytes = per_wg * wgs
+            regions = buf.numel() // nbytes
+            assert regions > EXTRA_CALLS // 4
 
-        def launch(i):
-            ptr = buf.data_ptr() + (i % regions) * nbytes
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            if lib.bz_bench_stream_read(ctypes.c_void_p(ptr), per_wg, wgs, ctypes.c_void_p(sink.data_ptr()),
-                                        ctypes.c_void_p(stream)) != 0:
-                raise RuntimeError("bz_bench_stream_read failed")
+            def launch(i):
+                ptr = buf.data_ptr() + (i % regions) * nbytes
+                stream = torch.cuda.current_stream(dev).cuda_stream
+                if lib.bz_bench_stream_read(ctypes.c_void_p(ptr), per_wg, wgs, ctypes.c_void_p(sink.data_ptr()),
+                                            ctypes.c_void_p(stream)) != 0:
+                    raise RuntimeError("bz_bench_stream_read failed")
 
-        def lead():
-            for i in (regions - 2, regions - 1):
-                launch(i)
+            def lead():
+                for i in (regions - 2, regions - 1):
+                    launch(i)
 
-        def timed():
-            for i in range(EXTRA_CALLS):
-                launch(i)
-        res[wgs] = time_captured(capture_timed(timed, dev, lead=lead), dev) / EXTRA_CALLS
+            def timed():
+                for i in range(EXTRA_CALLS):
+                    launch(i)
+            res[wgs] = time_captured(capture_timed(timed, dev, lead=lead), dev) / EXTRA_CALLS
+        out[name] = (res, nbytes)
     del buf
     torch.cuda.empty_cache()
-    return res, nbytes
+    return out
 
 
 def make_backbone(dev):
@@ -683,18 +690,20 @@ def main():
                 "pct_of_peak_hbm": round(100.0 * nbx / us_x / 1e3 / PEAK_HBM_GBS, 1), "bytes": nbx, "sets": nsx,
                 "rotated_bytes": rotx, "calls": EXTRA_CALLS}
             print(f"[bench] config {cfg} fused cold: {us_x:.3f} us/call", file=sys.stderr, flush=True)
+        sizes = {f"config{xc}_bytes": workloads.algorithmic_bytes(workloads.make(xc).seq_lens.tolist(), 16, 8, 128)
+                 for xc in (2, 3, 4)}
+        sizes.update(BACKBONE_GEMV_BYTES)
         floor = {}
-        for xc in (2, 3, 4):
-            nb = workloads.algorithmic_bytes(workloads.make(xc).seq_lens.tolist(), 16, 8, 128)
-            fl, nbf = time_stream_floor(dev, nb)
+        for name, (fl, nbf) in time_stream_floor(dev, sizes).items():
             best = min(fl.values())
-            floor[f"config{xc}_bytes"] = {
+            floor[name] = {
                 "bytes": nbf, "us_per_launch": {str(k): round(v, 3) for k, v in fl.items()},
                 "best_us": round(best, 3), "best_GB/s": round(nbf / best / 1e3, 1),
                 "best_pct_of_peak_hbm": round(100.0 * nbf / best / 1e3 / PEAK_HBM_GBS, 1)}
-            print(f"[bench] stream floor, config {xc} bytes: {fl}", file=sys.stderr, flush=True)
-        floor["method"] = ("a pure streaming read of the config's algorithmic bytes (no arithmetic, no exchange), "
-                           "timed like the cold calls; keyed by workgroup count")
+            print(f"[bench] stream floor, {name}: {fl}", file=sys.stderr, flush=True)
+        floor["method"] = ("a pure streaming read of the same bytes (no arithmetic, no exchange): the configs' "
+                           "algorithmic bytes and the backbone GEMVs' weight bytes, timed like the cold calls; "
+                           "keyed by workgroup count")
         extra["stream_floor"] = floor
         us_f, fb = time_depth_frame(pkg, dev)
         extra["config5_depth_frame"] = {"us_per_frame": round(us_f, 3), "us_per_call": round(us_f / 32, 3),
