@@ -19,7 +19,7 @@ from oracle.bf16 import f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 
-SEEDS = list(range(160))
+SEEDS = list(range(400))
 
 
 def draw(seed):
@@ -105,7 +105,7 @@ def test_random_case(device, seed):
                     assert not got[b, t].any(), f"{name} {what}: row {b} token {t} attends nothing but is not zero"
 
 
-FUSED_SEEDS = list(range(48))
+FUSED_SEEDS = list(range(120))
 
 
 @pytest.mark.parametrize("seed", FUSED_SEEDS)
