@@ -152,24 +152,25 @@ __device__ __forceinline__ uint4 lane_fetch4(const uint4& x, int src_lane) {
                     (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)x.z), (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)x.w));
 }
 
-// Clamp the row's range so that no access can leave [0, capacity).
+// The row's range from its raw seq_lens / kv_start values, clamped so that no access can leave [0, capacity).
+__device__ __forceinline__ void clamp_range(const Params& p, int e_raw, int s_raw, int& start, int& end) {
+  const int e = e_raw < 0 ? 0 : (e_raw > p.cap ? p.cap : e_raw);
+  start = p.kv_start == nullptr || s_raw < 0 ? 0 : (s_raw > e ? e : s_raw);
+  end = e;
+}
+
 __device__ __forceinline__ void row_range(const Params& p, int b, int& start, int& end) {
   // both loads are issued before either is waited for: without kv_start the second one reads seq_lens again and its
   // value is dropped (a conditional load would wait for the first before issuing the second)
   const int32_t* ks = p.kv_start ? p.kv_start : p.seq_lens;
-  int e = p.seq_lens[b];
-  int s = ks[b];
-  e = e < 0 ? 0 : (e > p.cap ? p.cap : e);
-  s = p.kv_start == nullptr || s < 0 ? 0 : (s > e ? e : s);
-  start = s;
-  end = e;
+  clamp_range(p, p.seq_lens[b], ks[b], start, end);
 }
 
-// Range of query token t of row b: the row's tokens are its last T positions, each attending up to itself, so token
-// t ends T - 1 - t positions before the row (flash/csrc/depth_frame.cu:221-227: token t of step 0 attends 0..t).
-__device__ __forceinline__ void token_range(const Params& p, int b, int t, int& start, int& end) {
-  row_range(p, b, start, end);
-  end = max(start, end - (p.T - 1 - t));
+// Range of query token t of a row whose range is [start, end): the row's tokens are its last T positions, each
+// attending up to itself, so token t ends T - 1 - t positions before the row (flash/csrc/depth_frame.cu:221-227:
+// token t of step 0 attends 0..t).
+__device__ __forceinline__ int token_end(const Params& p, int t, int start, int end) {
+  return max(start, end - (p.T - 1 - t));
 }
 
 // A row whose K+V span is at most kOneSplitBytes runs as one split whatever the grid: the cross-workgroup merge of two
@@ -415,7 +416,7 @@ __device__ __forceinline__ void unit_range(const Params& p, int b, int t, int& s
   } else {
     mask_row_range<NT, MK>(p, b, start, end, bits);
   }
-  end = max(start, end - (p.T - 1 - t));
+  end = token_end(p, t, start, end);
 }
 
 // One tile of KV rows held in VGPRs: position pos0 + ROWS * i for i < PPT (pos0 = tile start + this lane's row).
@@ -554,6 +555,15 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   uint4 qr[G];
   uint4 xe[NS], we[NS], xv, rc, rs;
   int64_t newpos64 = -1;
+  // The row's length and start first, ahead of every vector load of the workgroup: the CU's vector memory queue is
+  // shared with the workgroups already streaming there (four per CU on a 1024-workgroup grid), and a q load waiting
+  // for room in it would hold up these scalar loads behind it in program order.
+  int e_raw = 0, s_raw = 0;
+  if (MK == BZ_MASK_NONE) {
+    e_raw = p.seq_lens[b];
+    s_raw = (p.kv_start ? p.kv_start : p.seq_lens)[b];  // without kv_start: read again and dropped
+    __builtin_amdgcn_sched_barrier(0);
+  }
   if (FUSED) {
     const uint16_t* row = p.qkv + (int64_t)b * p.qkv_sb + 8 * c;
 #pragma unroll
@@ -581,7 +591,8 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
     // without a mask the row's range always comes from seq_lens (the host passes it); keeping the mask scan out of
     // this instantiation takes 2.3 KB of never-run code out of the kernel (5.9 KB instead of 8.2 at the serving
     // shape), which measured 2-4% faster
-    token_range(p, b, tok, start, end);
+    clamp_range(p, e_raw, s_raw, start, end);
+    end = token_end(p, tok, start, end);
   } else {
     unit_range<NT, MK>(p, b, tok, start, end, s_valid);
   }

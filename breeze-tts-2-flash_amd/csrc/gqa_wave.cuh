@@ -157,7 +157,7 @@ __global__ void __launch_bounds__(kWave) gqa_wave_kernel(const bz::Params p) {
   a.scale_log2 = scale_log2;
   a.out = out + (int64_t)b * o_sb + (int64_t)tok * o_st + (int64_t)hq * o_sh;
   attend_wave<D>(a, [&](int& start, int& end) {
-    // row_range and token_range on the values above; both loads are issued before either is waited for (without
+    // clamp_range and token_end on the values above; both loads are issued before either is waited for (without
     // kv_start the second reads seq_lens again and its value is dropped)
     int e = lens[b];
     int s = (starts ? starts : lens)[b];
