@@ -169,8 +169,24 @@ __device__ __forceinline__ void load_residual(const GemvParams& p, int row0, int
 
 // KC > 0: x held in registers, KC chunks per lane (k <= 512 KC <= 2 tiles): no LDS, and the RMSNorm's sum of squares
 // is reduced over the wave, so the prologue needs no barrier. KC == 0: x staged in LDS (any k).
+// What the first loads need (the weight segments, their row counts, k, x and its stride) comes as leading scalar
+// arguments, 56 bytes, which kernel-argument preloading (-mllvm -amdgpu-kernarg-preload-count) puts in SGPRs when the
+// wave starts, so the weight and x loads go out at once rather than after a load of the argument buffer; they are
+// the block's fields again, which the kernel then reads from these arguments.
 template <int M, int R, bool NORM, int EPI, int KC, int GAP>
-__global__ void __launch_bounds__(gemv_threads<KC>()) gemv_kernel(const GemvParams p) {
+__global__ void __launch_bounds__(gemv_threads<KC>())
+    gemv_kernel(const uint16_t* w0, const uint16_t* w1, const uint16_t* w2, int n0, int n1, int ntot, int k,
+                const uint16_t* x, int64_t ldx, const GemvParams args) {
+  GemvParams p = args;
+  p.w0 = w0;
+  p.w1 = w1;
+  p.w2 = w2;
+  p.n0 = n0;
+  p.n1 = n1;
+  p.ntot = ntot;
+  p.k = k;
+  p.x = x;
+  p.ldx = ldx;
   static_assert(GAP == 0 || KC > 0, "issue pacing on the x-in-registers path only");
   constexpr int NT = gemv_threads<KC>(), NW = NT / kWave;
   constexpr int NR = EPI == BZ_GEMV_SILU_MUL ? 2 * R : R;  // weight rows per wave
@@ -389,7 +405,8 @@ __global__ void __launch_bounds__(kGemvThreads) rmsnorm_kernel(const uint16_t* x
 
 // ---------------------------------------------------------------------------------------------- host side
 
-using GemvFn = void (*)(const GemvParams);
+using GemvFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int, int, const uint16_t*,
+                        int64_t, const GemvParams);
 
 template <int M, int R, int KC, int GAP>
 GemvFn pick_epi(int epi, bool norm) {
@@ -517,7 +534,8 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   p.ldy = a->y_stride;
   p.res = static_cast<const uint16_t*>(a->res);
   p.ldr = a->res_stride;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), kc > 0 ? 0 : lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), kc > 0 ? 0 : lds, stream, p.w0, p.w1, p.w2, p.n0, p.n1, p.ntot,
+                     p.k, p.x, p.ldx, p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

@@ -23,7 +23,7 @@ SplitFn pick_split(int D, int G, int mk, int ppt, int nt, bool fused) {
   return nullptr;
 }
 
-SplitFn pick_combine(int D, int G) {
+CombineFn pick_combine(int D, int G) {
 #define BZ_COMBINE_CASE(DD, GG) \
   if (D == DD && G == GG) return gqa_combine_kernel<DD, GG>;
   BZ_COMBINE_CASE(128, 1) BZ_COMBINE_CASE(128, 2) BZ_COMBINE_CASE(128, 4) BZ_COMBINE_CASE(128, 8)
@@ -32,7 +32,8 @@ SplitFn pick_combine(int D, int G) {
   return nullptr;
 }
 
-using WaveFn = void (*)(const Params);
+using WaveFn = void (*)(const int32_t*, const int32_t*, const uint16_t*, const uint16_t*, int64_t, int64_t, int32_t,
+                        int32_t, const Params);
 
 WaveFn pick_wave(int D) {
   if (D == 128) return gqa_wave_kernel<128>;
@@ -208,7 +209,7 @@ int launch_wave(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* 
   if (rows_of(a) > 65535) return BZ_ERR_SHAPE;  // one workgroup per wave: grid (G, NKV, rows), grid.z <= 65535
   const Params p = base_params(a, seq_lens, kv_start);
   hipLaunchKernelGGL(fn, dim3(a->num_q_heads / a->num_kv_heads, a->num_kv_heads, rows_of(a)), dim3(kWave), 0, stream,
-                     p);
+                     p.seq_lens, p.kv_start, p.k, p.v, p.kv_sb, p.kv_sh, (int32_t)p.kv_ss, p.cap, p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
@@ -329,7 +330,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   const int nt = kSplitThreads;
   const int ppt = ppt_for(D, G, chunk, nt);
   SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt, f != nullptr);
-  SplitFn comb_fn = pick_combine(D, G);
+  CombineFn comb_fn = pick_combine(D, G);
   if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
   bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
   if (!two_kernels && splits > 1) {
@@ -371,7 +372,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
     p.v_out = const_cast<uint16_t*>(p.v);
   }
 
-  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, R), dim3(nt), 0, stream, p);
+  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, R), dim3(nt), 0, stream, p.seq_lens, p.kv_start, p);
   if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
   if (two_kernels && splits > 1) {
     hipLaunchKernelGGL(comb_fn, dim3(NKV, R), dim3(kThreads), 0, stream, p);

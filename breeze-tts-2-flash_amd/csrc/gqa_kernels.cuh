@@ -72,7 +72,13 @@ struct Params {
   uint16_t* v_out;
 };
 
-using SplitFn = void (*)(const Params);
+// The split kernels take the rows' range arrays (seq_lens, kv_start) as leading kernel arguments ahead of the
+// parameter block: built with kernel-argument preloading (-mllvm -amdgpu-kernarg-preload-count), the leading scalar
+// arguments of a kernel (up to 56 bytes; a struct argument is never preloaded) arrive in SGPRs with the wave, so the
+// range loads go out at once instead of after a load of the argument buffer. Without preloading they are read from
+// the argument buffer like the rest.
+using SplitFn = void (*)(const int32_t*, const int32_t*, const Params);
+using CombineFn = void (*)(const Params);
 
 // Kernel tables (gqa_fused.hip defines the fused one).
 SplitFn pick_split_fused(int D, int G, int mk, int ppt, int nt);
@@ -83,6 +89,7 @@ namespace {
 
 using bz::Params;
 using bz::SplitFn;
+using bz::CombineFn;
 
 
 constexpr int kThreads = 256;  // 4 wave64 (merge and mask kernels)
@@ -531,8 +538,9 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
 
 // ---------------------------------------------------------------------------------------------- kernels
 
+// lens, starts: p.seq_lens and p.kv_start again, as leading (preloaded) arguments.
 template <int D, int G, int PPT, int MK, int NT, bool FUSED>
-__global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
+__global__ void __launch_bounds__(NT) gqa_split_kernel(const int32_t* lens, const int32_t* starts, const Params p) {
   constexpr int NW = NT / kWave;        // waves per workgroup
   constexpr int LPR = D / 8;            // lanes per KV row, 16 B (8 bf16) each
   constexpr int ROWS = NT / LPR;        // KV rows per load instruction across the workgroup
@@ -557,11 +565,12 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const Params p) {
   int64_t newpos64 = -1;
   // The row's length and start first, ahead of every vector load of the workgroup: the CU's vector memory queue is
   // shared with the workgroups already streaming there (four per CU on a 1024-workgroup grid), and a q load waiting
-  // for room in it would hold up these scalar loads behind it in program order.
+  // for room in it would hold up these scalar loads behind it in program order. Their addresses come from the
+  // preloaded leading arguments, so the loads do not wait for the argument buffer.
   int e_raw = 0, s_raw = 0;
   if (MK == BZ_MASK_NONE) {
-    e_raw = p.seq_lens[b];
-    s_raw = (p.kv_start ? p.kv_start : p.seq_lens)[b];  // without kv_start: read again and dropped
+    e_raw = lens[b];
+    s_raw = (starts ? starts : lens)[b];  // without kv_start: read again and dropped
     __builtin_amdgcn_sched_barrier(0);
   }
   if (FUSED) {

@@ -129,20 +129,21 @@ __device__ void attend_wave(const WaveAttention& a, Range range) {
 // to itself), then attend_wave. One wave per workgroup, so the waves spread over as many CUs as there are
 // (config-5 frame with one wave per kv head: 102 us against 111 with four waves per workgroup, 108 with two).
 // Grid (group size G, kv heads, rows * T): the launch covers exactly the waves, and the head indices need no division.
+// What the first loads need (the range arrays, the K / V bases, strides and capacity) comes as leading scalar
+// arguments, 56 bytes, which kernel-argument preloading puts in SGPRs when the wave starts: the K / V tiles and the
+// range loads then go out at once rather than after a load of the argument buffer (they are p's fields again; kv_ss
+// fits 32 bits, as the host bounds capacity * kv_stride_s).
 template <int D>
-__global__ void __launch_bounds__(kWave) gqa_wave_kernel(const bz::Params p) {
-  // every kernel argument the wave reads is loaded before any of them is used, so that the loads go out together:
-  // one round trip to the argument buffer instead of one per group of dependent uses
+__global__ void __launch_bounds__(kWave) gqa_wave_kernel(const int32_t* lens, const int32_t* starts, const uint16_t* k,
+                                                         const uint16_t* v, int64_t kv_sb, int64_t kv_sh, int32_t kv_ss,
+                                                         int32_t cap, const bz::Params p) {
+  // every other kernel argument the wave reads is loaded before any of them is used, so that the loads go out
+  // together: one round trip to the argument buffer instead of one per group of dependent uses
   const uint16_t* const q = p.q;
   const int64_t q_sb = p.q_sb, q_sh = p.q_sh, q_st = p.q_st;
-  const uint16_t* const k = p.k;
-  const uint16_t* const v = p.v;
-  const int64_t kv_sb = p.kv_sb, kv_sh = p.kv_sh, kv_ss = p.kv_ss;
-  const int32_t* const lens = p.seq_lens;
-  const int32_t* const starts = p.kv_start;
   uint16_t* const out = p.out;
   const int64_t o_sb = p.o_sb, o_sh = p.o_sh, o_st = p.o_st;
-  const int T = p.T, cap = p.cap, G = p.G;
+  const int T = p.T, G = p.G;
   const float scale_log2 = p.scale_log2;
   __builtin_amdgcn_sched_barrier(0);
 
