@@ -52,6 +52,8 @@ def parse_args():
     p.add_argument("--depth-only", action="store_true",
                    help="only the depth frames: config 5 (split and wave kernels) and the real depth shape")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--per-call", type=int, default=0, metavar="N",
+                   help="only the distribution of N single cold calls of --config (a GPU stamp before every call)")
     p.add_argument("--traffic-bytes", type=float, default=None,
                    help="HBM bytes per call (overrides the value read from profiles/)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -266,6 +268,60 @@ STREAM_WGS = (256, 512, 1024)
 # weight bytes of the backbone's GEMVs (bf16, hidden 2048, 16 q / 8 KV heads of 128, intermediate 6144)
 BACKBONE_GEMV_BYTES = {"gemv_qkv_norm_bytes": 2 * 4096 * 2048, "gemv_o_resid_bytes": 2 * 2048 * 2048,
                        "gemv_gateup_norm_silu_bytes": 2 * 2 * 6144 * 2048, "gemv_down_resid_bytes": 2 * 2048 * 6144}
+
+
+def per_call_times(pkg, w, dev, calls):
+    """The distribution of single cold calls of workload w: one HIP graph holding a GPU stamp before every call (and
+    one after the last), rotating over ROTATE_BYTES of K/V sets, replayed twice after a cache flush; each interval
+    between stamps is one stamp launch plus one call, and the median interval of a graph of stamps alone is
+    subtracted. Returns a dict of µs figures (mean, percentiles, a 0.25 µs histogram)."""
+    import numpy as np
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    g = w.to(dev)
+    read_bytes = workloads.algorithmic_bytes(w.seq_lens.tolist(), w.num_q_heads, w.num_kv_heads, w.head_dim)
+    nsets = max(16, math.ceil(ROTATE_BYTES / read_bytes)) + 2
+    ks = torch.empty((nsets,) + tuple(g.k.shape), dtype=g.k.dtype, device=dev)
+    vs = torch.empty_like(ks)
+    ks.copy_(g.k.expand_as(ks))
+    vs.copy_(g.v.expand_as(vs))
+    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
+
+    def call(i):  # sets 0 and 1 for the two lead calls, then 2 .. nsets - 1 in turn
+        j = 2 + i % (nsets - 2) if i >= 0 else i + 2
+        pkg.gqa_decode(g.q, ks[j], vs[j], g.seq_lens, g.scale, out)
+
+    def intervals(body, flush):
+        st = GpuStamps(dev, n=calls + 1)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            body(-2)
+            body(-1)
+            for i in range(calls):
+                st.stamp(i)
+                body(i)
+            st.stamp(calls)
+        graph.replay()
+        torch.cuda.synchronize()
+        res = []
+        for _ in range(2):
+            if flush:
+                flush_caches(dev)
+            graph.replay()
+            torch.cuda.synchronize()
+            res.append(np.diff(np.array(st.buf.cpu().tolist(), dtype=np.float64)) * st.us_per_tick)
+        return np.concatenate(res)
+
+    stamp_us = float(np.median(intervals(lambda i: None, False)))
+    d = intervals(call, True) - stamp_us
+    del ks, vs
+    torch.cuda.empty_cache()
+    lo = math.floor(d.min() * 4) / 4
+    hist, edges = np.histogram(d, bins=np.arange(lo, d.max() + 0.25, 0.25))
+    pct = {f"p{q}": round(float(np.percentile(d, q)), 3) for q in (1, 10, 50, 90, 99)}
+    return {"calls": int(d.size), "stamp_launch_us": round(stamp_us, 3), "mean": round(float(d.mean()), 3), **pct,
+            "histogram_0.25us": [[round(float(a), 2), int(c)] for a, c in zip(edges, hist) if c]}
 
 
 def time_stream_floor(dev, sizes):
@@ -637,6 +693,10 @@ def main():
               flush=True)
         return
     cfg = args.config
+    if args.per_call:
+        print(json.dumps({"per_call_us": per_call_times(pkg, workloads.make(cfg), dev, args.per_call),
+                          "config": cfg}), flush=True)
+        return
     w2 = workloads.make(cfg)
     splits2 = args.splits or pkg.default_splits(w2.batch, w2.num_kv_heads, w2.head_dim, w2.capacity, 0)
     print(f"[bench] config {cfg} cold, {args.steps} calls, splits={splits2}, combine={args.combine}", file=sys.stderr,
