@@ -41,3 +41,18 @@ def test_more_than_one_gpu_is_refused(n):
                        text=True, timeout=300, cwd=ROOT)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_default_arguments_and_modes(monkeypatch):
+    """No flags: one GPU, 1000 timed calls after 50 warm-ups, config 2, the library's defaults; the diagnostic modes
+    parse to their own flags (none of them is on by default)."""
+    monkeypatch.setattr(sys, "argv", ["bench.py"])
+    a = bench.parse_args()
+    assert (a.gpus, a.steps, a.warmup, a.config, a.splits, a.combine) == (1, 1000, 50, 2, 0, "auto")
+    assert not (a.per_call or a.backbone_only or a.depth_only or a.fused or a.eager or a.no_extra or a.no_cpu)
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--per-call", "400", "--config", "3"])
+    a = bench.parse_args()
+    assert (a.per_call, a.config) == (400, 3)
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "1", "--steps", "20", "--warmup", "5"])  # the driver's
+    a = bench.parse_args()
+    assert (a.gpus, a.steps, a.warmup) == (1, 20, 5)
