@@ -24,6 +24,10 @@
 #include "bz_gemv.h"
 #include "device_common.cuh"
 
+namespace bz {
+int device_cu_count(int* cus);  // gqa_decode.hip: the current device's CU count, cached per device
+}  // namespace bz
+
 namespace {
 
 constexpr int kGemvThreads = 256;              // 4 waves per workgroup (x in registers; rmsnorm)
@@ -38,15 +42,19 @@ constexpr int kU = 2;                          // chunks per tile
 constexpr int kTileK = kChunk * kU;            // k elements per tile
 constexpr int kMaxLds = 64 * 1024;             // bytes of LDS for x
 // With x in registers every wave issues all its weight loads at once; spacing them by s_sleep(kIssueGap) (about
-// 64 * kIssueGap clocks) measured faster: q|k|v 5.06 against 5.19 us, gate/up 10.0 against 10.3-10.5. Gaps of 1, 3, 4
-// and 6 were tried; 2 was best or within noise of best. It pays only when many workgroups contend for the memory
-// system; a small grid just waits longer for its last load (gate/up, M = 2, k = 2048: 12 workgroups 3.43 against
-// 2.89 us, 32 workgroups 4.05 against 3.92, 128 workgroups 4.25 against 4.43), so the host picks the paced variant
-// (GAP = kIssueGap) for grids of at least kPaceMinGrid workgroups. The gap is a template parameter, not a runtime
-// flag: a branch around each s_sleep split the loads over basic blocks, and the compiler's wait counts then went
-// pessimistic (the prologue waited for three more weight loads than it needs).
+// 64 * kIssueGap clocks) measured faster where the loads queue: q|k|v 5.06 against 5.19 us, gate/up 10.0 against
+// 10.3-10.5. Gaps of 1, 3, 4 and 6 were tried; 2 was best or within noise of best. A small grid just waits longer for
+// its last load (gate/up, M = 2, k = 2048: 12 workgroups 3.43 against 2.89 us, 32 workgroups 4.05 against 3.92, 128
+// workgroups 4.25 against 4.43), and so does a grid of one workgroup per CU whose waves issue few loads (o_proj, 256
+// workgroups of eight 1 KiB loads per wave: 3.31 us unpaced against 3.64 paced; q|k|v at two workgroups per CU 4.89
+// either way; gate/up, 16 loads per wave, 9.68 paced against 9.96). So the host picks the paced variant (GAP =
+// kIssueGap) for grids of at least kPaceMinGrid workgroups whose waves issue at least kPaceMinLoads weight loads each
+// or that hold more workgroups than the device has CUs. The gap is a template parameter, not a runtime flag: a branch
+// around each s_sleep split the loads over basic blocks, and the compiler's wait counts then went pessimistic (the
+// prologue waited for three more weight loads than it needs).
 constexpr int kIssueGap = 2;
 constexpr int kPaceMinGrid = 64;
+constexpr int kPaceMinLoads = 16;
 
 struct GemvParams {
   const uint16_t* x;
@@ -515,7 +523,14 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   const int threads = kc > 0 ? kGemvThreads : kGemvLdsThreads;
   const int rows_per_block = threads / kWave * r;
   const int grid = (ntot + rows_per_block - 1) / rows_per_block;
-  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr, grid >= kPaceMinGrid);
+  bool pace = kc > 0 && grid >= kPaceMinGrid;
+  if (pace && (a->epilogue == BZ_GEMV_SILU_MUL ? 2 * r : r) * kc < kPaceMinLoads) {
+    int cus = 0;
+    const int rc = bz::device_cu_count(&cus);
+    if (rc != BZ_OK) return rc;
+    pace = grid > cus;
+  }
+  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr, pace);
   if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   GemvParams p;
   p.x = static_cast<const uint16_t*>(a->x);

@@ -447,6 +447,11 @@ int launch_probs(const bz_gqa_decode_args* a, const bz_gqa_decode_fused_args* f,
 
 }  // namespace
 
+namespace bz {
+// The CU count of the current device (cached per device), for the GEMVs' launch choices in gemv.hip.
+int device_cu_count(int* cus) { return device_cus(cus); }
+}  // namespace bz
+
 extern "C" {
 
 __attribute__((visibility("default"))) int bz_gqa_decode(const bz_gqa_decode_args* a, hipStream_t stream) {
