@@ -49,6 +49,8 @@ def parse_args():
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--backbone-only", action="store_true",
                    help="only the 28-layer backbone decode step and its GEMVs (for profiling)")
+    p.add_argument("--backbone-m", type=int, nargs="+", default=[2], choices=[1, 2, 4],
+                   help="rows of the --backbone-only step (default 2, the CFG pair)")
     p.add_argument("--depth-only", action="store_true",
                    help="only the depth frames: config 5 (split and wave kernels) and the real depth shape")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -98,6 +100,7 @@ EXTRA_CALLS = 1000          # timed calls of each extra workload, whatever --ste
 EXTRA_FRAMES = 200          # timed depth frames
 BACKBONE_REPS = 100         # timed backbone steps (and replays of each GEMV's 28-layer graph)
 BACKBONE_CHAIN = 5          # steps per replay for the back-to-back backbone figure
+BACKBONE_REPS_OTHER_M = 30  # timed backbone steps at M = 1 and 4
 
 _FLUSH = {}
 
@@ -217,10 +220,12 @@ def time_calls(pkg, w, dev, steps, warmup, combine, splits, eager, cold, fused=F
     kw = dict(combine=combine, num_splits=splits)
     if fused:
         qkv, qn, kn, cos, sin, cache_pos = fused_inputs(w, dev)
+        # the fused entry is captured with a workspace made beforehand (a capture allocates nothing)
+        ws = pkg.get_workspace(dev, w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.capacity, splits)
 
         def run(k, v, o=None):
             return pkg.gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, k, v, cache_pos, g.scale, o, seq_lens=g.seq_lens,
-                                        **kw)
+                                        workspace=ws, **kw)
     else:
         def run(k, v, o=None):
             return pkg.gqa_decode(g.q, k, v, g.seq_lens, g.scale, o, **kw)
@@ -369,14 +374,14 @@ def time_stream_floor(dev, sizes):
     return out
 
 
-def make_backbone(dev):
+def make_backbone(dev, M=2):
     """Random-init weights, KV caches and buffers of the reference's backbone at its serving shape (a Qwen3 of hidden
-    2048, 16 q / 8 KV heads of 128, intermediate 6144, 28 layers; the CFG pair, M = 2; KV 1024 of 2048 slots)."""
+    2048, 16 q / 8 KV heads of 128, intermediate 6144, 28 layers; KV 1024 of 2048 slots) for M rows: 2 is the CFG
+    pair, 1 and 4 the other batch sizes the reference's fused step takes (flash/backbone.py:18-22, :58)."""
     import torch
 
     c = BACKBONE
     H, nq, nk, I, L, D = c["H"], c["nq"], c["nk"], c["inter"], c["layers"], c["D"]
-    M = 2
     gen = torch.Generator(device=dev).manual_seed(123)
     bf = torch.bfloat16
 
@@ -406,32 +411,33 @@ def make_backbone(dev):
     sin = ang.sin().to(bf).expand(M, D).contiguous().to(dev)
     cache_pos = torch.tensor([pos], dtype=torch.int64, device=dev)
     lens = torch.full((M,), c["len"], dtype=torch.int32, device=dev)
-    return dict(layers=layers, norm_w=norm_w, x0=x0, qkv=qkv, ao=ao, h1=h1, act=act, xb=xb, hidden=hidden, cos=cos,
-                sin=sin, cache_pos=cache_pos, lens=lens)
+    return dict(M=M, layers=layers, norm_w=norm_w, x0=x0, qkv=qkv, ao=ao, h1=h1, act=act, xb=xb, hidden=hidden,
+                cos=cos, sin=sin, cache_pos=cache_pos, lens=lens)
 
 
-def time_backbone(pkg, dev, reps=BACKBONE_REPS, model=None):
-    """The backbone decode step of make_backbone (or `model`, made earlier by it): per layer gemv_seg (RMSNorm +
-    q|k|v) -> gqa_decode_fused -> gemv_resid (o_proj) -> gemv_gateup -> gemv_resid (down), then the final rmsnorm
+def time_backbone(pkg, dev, reps=BACKBONE_REPS, model=None, M=2):
+    """The backbone decode step of make_backbone(dev, M) (or `model`, made earlier by it): per layer gemv_seg (RMSNorm
+    + q|k|v) -> gqa_decode_fused -> gemv_resid (o_proj) -> gemv_gateup -> gemv_resid (down), then the final rmsnorm
     (flash/backbone.py:120-129), one HIP graph per step. Also each GEMV alone, rotating over the 28 layers' weights.
     Returns {name: {us, bytes, GB/s}}."""
     import torch
 
     c = BACKBONE
     H, nq, nk, I, L, D = c["H"], c["nq"], c["nk"], c["inter"], c["layers"], c["D"]
-    M = 2
-    m = model if model is not None else make_backbone(dev)
+    m = model if model is not None else make_backbone(dev, M)
+    M = m["M"]
     layers, norm_w, x0, qkv, ao, h1, act, xb, hidden = (m[k] for k in ("layers", "norm_w", "x0", "qkv", "ao", "h1",
                                                                          "act", "xb", "hidden"))
     cos, sin, cache_pos, lens = m["cos"], m["sin"], m["cache_pos"], m["lens"]
     eps, scale = 1e-6, D ** -0.5
+    ws = pkg.get_workspace(dev, M, nq // D, nk // D, D, c["cap"])  # made before the step is captured
 
     def step():
         x = x0
         for i, ly in enumerate(layers):
             pkg.gemv_seg(x, ly["ln1"], eps, ly["wq"], ly["wk"], ly["wv"], qkv)
             pkg.gqa_decode_fused(qkv, ly["qn"], ly["kn"], eps, cos, sin, ly["kc"], ly["vc"], cache_pos, scale, ao,
-                                 seq_lens=lens)
+                                 seq_lens=lens, workspace=ws)
             pkg.gemv_resid(ao.view(M, nq), ly["wo"], x, h1)
             pkg.gemv_gateup(h1, ly["ln2"], eps, ly["wg"], ly["wu"], act)
             pkg.gemv_resid(act, ly["wd"], h1, xb[i % 2])
@@ -681,7 +687,7 @@ def main():
     pkg.load()
 
     if args.backbone_only:
-        bb = time_backbone(pkg, dev)
+        bb = {f"m{M}": time_backbone(pkg, dev, M=M) for M in args.backbone_m}
         print(json.dumps({"backbone": bb}), flush=True)
         return
     if args.depth_only:
@@ -789,6 +795,14 @@ def main():
         extra["backbone"] = bb
         for k, v in bb.items():
             print(f"[bench] {k}: {v}", file=sys.stderr, flush=True)
+        # the reference's other served batch sizes (its fused step takes M in {1, 2, 4}, flash/backbone.py:18-22, :58)
+        for M in (1, 4):
+            bbm = time_backbone(pkg, dev, reps=BACKBONE_REPS_OTHER_M, M=M)
+            bbm["timing"] = (f"as backbone, M = {M}: median of {BACKBONE_REPS_OTHER_M} flushed replays; back_to_back "
+                             f"median of {max(3, BACKBONE_REPS_OTHER_M // 10)}")
+            extra[f"backbone_m{M}"] = bbm
+            print(f"[bench] backbone M={M}: step {bbm['backbone_step_28_layers']['us']} us", file=sys.stderr,
+                  flush=True)
         ho = host_overhead(pkg, dev)
         ho["method"] = (f"eager host µs per call: {HOST_CALLS} back-to-back calls without a synchronisation, config 1 "
                         f"inputs (GEMV 2x1024x1024), median of 5 samples")

@@ -6,6 +6,10 @@ scaling, ...), with seq_lens in the mask's place. Every call goes through the C 
 guard. Workspaces are cached per (device, stream), as the reference caches its _workspace (flash/backbone.py:27-37),
 so a call allocates nothing once its stream's workspace is large enough and can be recorded into a HIP graph.
 
+Nothing here allocates device memory while the current stream is being captured into a HIP graph: a non-fused call
+without a workspace then runs on the library's static scratch (bz_gqa_decode_noalloc), and a fused call without one
+raises (pass workspace=, from get_workspace() made before the capture).
+
 Errors follow the reference (TORCH_CHECK -> RuntimeError, bb_attn.cu:377-388, :420-447).
 """
 from __future__ import annotations
@@ -77,8 +81,9 @@ def get_workspace(device: torch.device, batch: int, num_q_heads: int, num_kv_hea
     capacity or length. There is one per (device, stream, groups), because calls in flight on two streams must not
     share counters and partials. A call that needs more room replaces it with a zeroed one at least twice as large;
     the replaced one stays allocated (a captured graph may still use it), so the memory held stays under twice the
-    largest need. A call without a workspace made while its stream is being captured into a HIP graph does not come
-    here: it runs on the library's static scratch (bz_gqa_decode_noalloc)."""
+    largest need. Call this before capturing a graph that makes fused calls, and pass the result as workspace=:
+    nothing is allocated while a stream is being captured (a non-fused call without a workspace then runs on the
+    library's static scratch instead)."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     return kernels.run_on(torch.device("cuda", idx), lambda stream: _stream_workspace(
         idx, stream, batch, num_q_heads, num_kv_heads, head_dim, capacity, num_splits, max_seq_len))
@@ -93,17 +98,47 @@ def _stream_workspace(idx: int, stream: int, batch: int, num_q_heads: int, num_k
     ws = _WS.get(key)
     if ws is not None and ws.numel() >= n:
         return ws
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"gqa_decode: no workspace of {n} bytes exists for the stream being captured, and nothing is allocated "
+            "during a capture: pass workspace= (attention.get_workspace(...), made before the capture)")
     with _WS_LOCK:
         ws = _WS.get(key)
         if ws is None or ws.numel() < n:
             size = n if ws is None else max(n, 2 * ws.numel())
-            new = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", idx))
+            new = _zeroed_outside_pools(size, idx)
             if new.data_ptr() % 256:
                 raise RuntimeError("workspace allocation is not 256-byte aligned")
             if ws is not None:
                 _WS_RETIRED.append(ws)
             _WS[key] = ws = new
         return ws
+
+
+def _zeroed_outside_pools(nbytes: int, idx: int) -> torch.Tensor:
+    """A zero-filled uint8 tensor of nbytes on device idx, allocated by a helper thread: torch.compile's CUDA-graph
+    trees route every allocation of the thread that warms a graph up into that graph's private pool, and a workspace
+    cached across calls must not live there (the trees check that the pool holds only the graph's outputs). The zero
+    fill runs on a stream of the helper thread and has completed when this returns."""
+    box = []
+
+    def make():
+        try:
+            dev = torch.device("cuda", idx)
+            side = torch.cuda.Stream(dev)
+            with torch.cuda.stream(side):
+                t = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+            side.synchronize()
+            box.append(t)
+        except BaseException as e:  # re-raised in the calling thread
+            box.append(e)
+
+    th = threading.Thread(target=make, name="bz-workspace")
+    th.start()
+    th.join()
+    if isinstance(box[0], BaseException):
+        raise box[0]
+    return box[0]
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -204,26 +239,24 @@ def _int32_rows(t: torch.Tensor, B: int, name: str, device) -> torch.Tensor:
     return t
 
 
-def _run(a, dev, workspace, entry: str, static_scratch: bool = False) -> None:
+def _run(a, dev, workspace, entry: str) -> None:
     """Launches bz_gqa_decode or bz_gqa_decode_masked (entry) on the device's current stream.
 
-    Without a workspace, a call made while that stream is being captured into a HIP graph, or with static_scratch
-    (the torch operators, which run inside compiled graphs), goes to bz_gqa_decode_noalloc: it uses the library's
-    static per-device scratch and allocates nothing. An allocation there would come from a graph's private pool,
-    which torch.compile's CUDA-graph trees require to hold only the graph's outputs (in their eager warm-up runs as
-    well as under capture). Calls on the scratch must not overlap in time on one device (graph replays or compiled
-    calls on several streams). Sizes beyond the scratch (BZ_ERR_SCRATCH) take the stream's cached workspace."""
+    Without a workspace, a call made while that stream is being captured into a HIP graph (a torch.cuda.graph, or
+    torch.compile's CUDA-graph trees recording) goes to bz_gqa_decode_noalloc: it uses the library's static per-device
+    scratch and allocates nothing. The graph then holds that scratch: its replays must not overlap in time with other
+    calls on the scratch on the same device. Sizes beyond the scratch (BZ_ERR_SCRATCH) raise under capture. Any other
+    call without a workspace takes the cached workspace of its (device, stream)."""
     lib = kernels.load()
 
     def launch(stream):
         sp = ctypes.c_void_p(stream)
-        if workspace is None and (static_scratch or torch.cuda.is_current_stream_capturing()):
+        if workspace is None and torch.cuda.is_current_stream_capturing():
             if entry == "bz_gqa_decode_masked":
                 a.seq_lens, a.kv_start = None, None  # the noalloc entry takes the range from the mask
-            rc = lib.bz_gqa_decode_noalloc(ctypes.byref(a), sp)
-            if rc != kernels.ERR_SCRATCH:
-                kernels.check(rc, "bz_gqa_decode_noalloc")
-                return
+            kernels.check(lib.bz_gqa_decode_noalloc(ctypes.byref(a), sp),
+                          "bz_gqa_decode_noalloc (a call captured without workspace=; pass one for these sizes)")
+            return
         ws = workspace if workspace is not None else _stream_workspace(
             dev.index, stream, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim,
             a.capacity, a.num_splits, a.max_seq_len)
@@ -265,7 +298,7 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
 
 
 def _gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_splits, max_seq_len, combine,
-                workspace, static_scratch=False) -> torch.Tensor:
+                workspace) -> torch.Tensor:
     """gqa_decode's call through the C ABI (the body of the eager path and of torch.ops.bz.gqa_decode)."""
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
@@ -275,7 +308,7 @@ def _gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_s
         _check(mask.device == dev, "mask must be on the query's device")
         a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
         a.mask = mask.data_ptr()
-    _run(a, dev, workspace, "bz_gqa_decode", static_scratch)
+    _run(a, dev, workspace, "bz_gqa_decode")
     return out
 
 
@@ -320,14 +353,14 @@ def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
 
 
 def _gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine,
-                       workspace, static_scratch=False) -> torch.Tensor:
+                       workspace) -> torch.Tensor:
     """gqa_decode_masked's call through the C ABI."""
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
     _check(mask.device == dev, "mask must be on the query's device")
     a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
     a.mask = mask.data_ptr()
-    _run(a, dev, workspace, "bz_gqa_decode_masked", static_scratch)
+    _run(a, dev, workspace, "bz_gqa_decode_masked")
     return out
 
 
@@ -344,9 +377,21 @@ def gqa_decode_probs(q: torch.Tensor, k_cache: torch.Tensor, seq_lens: torch.Ten
     """The softmax probabilities of the gqa_decode call with these arguments (bz_gqa_decode_probs): float32
     [B, NH, capacity], each bf16(exp(s - max) / sum) inside the row's range and 0 at excluded positions and outside
     it. seq_lens None: the range comes from the mask, as in gqa_decode_masked. The reference's optional dbg output of
-    attn_decode (bb_attn.cu:74, :288-289); a verification path, not a fast one. q: [B, NH, D] (one query token)."""
+    attn_decode (bb_attn.cu:74, :288-289); a verification path, not a fast one. q: [B, NH, D] (one query token).
+    Under torch.compile the call is the registered operator torch.ops.bz.gqa_decode_probs."""
     _check(q.dim() == 3 or (q.dim() == 4 and q.size(2) == 1), "gqa_decode_probs takes one query token per row")
-    a, _ = _fill_args(q, k_cache, k_cache, scale, None, 0, 0, "auto")
+    if probs is None:
+        probs = torch.empty(q.size(0), q.size(1), k_cache.size(2), dtype=torch.float32, device=q.device)
+    if torch.compiler.is_compiling():
+        torch.ops.bz.gqa_decode_probs(q, k_cache, seq_lens, float(scale), probs, kv_start, mask)
+        return probs
+    return _gqa_decode_probs(q, k_cache, seq_lens, scale, probs, kv_start, mask)
+
+
+def _gqa_decode_probs(q, k_cache, seq_lens, scale, probs, kv_start, mask) -> torch.Tensor:
+    """gqa_decode_probs's call through the C ABI. The probabilities need neither V nor an output: k_cache stands in
+    for v_cache and q for out in the argument struct (same shapes and layout checks; neither is read or written)."""
+    a, _ = _fill_args(q, k_cache, k_cache, scale, q, 0, 0, "auto")
     dev = q.device
     if seq_lens is not None:
         a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
@@ -357,8 +402,6 @@ def gqa_decode_probs(q: torch.Tensor, k_cache: torch.Tensor, seq_lens: torch.Ten
         _check(mask.device == dev, "mask must be on the query's device")
         a.mask_dtype, a.mask_stride_b = _mask_view(mask, a.batch, a.capacity)
         a.mask = mask.data_ptr()
-    if probs is None:
-        probs = torch.empty(a.batch, a.num_q_heads, a.capacity, dtype=torch.float32, device=dev)
     _check_probs(probs, a, dev)
     kernels.run_on(dev, lambda stream: kernels.check(kernels.load().bz_gqa_decode_probs(
         ctypes.byref(a), ctypes.c_void_p(probs.data_ptr()), ctypes.c_void_p(stream)), "bz_gqa_decode_probs"))
@@ -457,6 +500,8 @@ def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
     lib = kernels.load()
 
     def launch(stream):
+        # _stream_workspace raises rather than allocate while the stream is being captured (the fused entry has no
+        # static-scratch form: pass workspace= to capture it)
         ws = workspace if workspace is not None else _stream_workspace(
             dev.index, stream, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim,
             a.capacity, a.num_splits, a.max_seq_len)

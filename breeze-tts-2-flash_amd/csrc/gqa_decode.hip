@@ -7,7 +7,6 @@
 
 #include <atomic>
 #include <mutex>
-#include <unordered_map>
 
 #include "bz_gqa_decode.h"
 #include "gqa_kernels.cuh"
@@ -236,30 +235,6 @@ bool wave_route(const bz_gqa_decode_args* a, int mask_kind, const bz_gqa_decode_
          wave_out_aligned(a);
 }
 
-// Workgroups of `fn` (NT threads) that fit on the device at once: the split kernel's merger waits for the other
-// splits of its group, so a one-launch merge is only used when every workgroup of the grid can be resident together
-// (larger grids take the merge kernel). Cached per kernel; the device's CU count is cached per device.
-std::mutex g_occ_mu;
-std::unordered_map<const void*, int> g_occ;
-
-int resident_workgroups(SplitFn fn, int nt, int cus, long long* out) {
-  int per_cu = 0;
-  {
-    std::lock_guard<std::mutex> lk(g_occ_mu);
-    auto it = g_occ.find(reinterpret_cast<const void*>(fn));
-    if (it != g_occ.end()) per_cu = it->second;
-  }
-  if (per_cu == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), nt, 0) != hipSuccess ||
-        per_cu <= 0)
-      return BZ_ERR_DEVICE;
-    std::lock_guard<std::mutex> lk(g_occ_mu);
-    g_occ[reinterpret_cast<const void*>(fn)] = per_cu;
-  }
-  *out = (long long)per_cu * cus;
-  return BZ_OK;
-}
-
 // The static scratch of bz_gqa_decode_noalloc, for callers that cannot allocate (code under HIP graph capture,
 // torch.compile's CUDA-graph trees, serving loops that forbid allocation): device memory of the library itself, one
 // copy per device, held until the process ends. Its layout differs from a workspace's: the arrival counters of up to
@@ -290,8 +265,8 @@ int scratch_address(void** addr) {
   return BZ_OK;
 }
 
-// Picks the kernels, checks the workspace and launches the split kernel (and, when asked or when the grid cannot be
-// resident at once, the merge kernel), or the wave kernel where wave_route says so (it needs no workspace).
+// Picks the kernels, checks the workspace and launches the split kernel (and, when asked, the merge kernel), or the
+// wave kernel where wave_route says so (it needs no workspace).
 // seq_lens NULL: each row's range comes from the mask, scanned by the kernels themselves. f != nullptr selects the
 // fused-prologue variant. scratch_base != nullptr: the static scratch (its address on the current device) instead of
 // a->workspace.
@@ -332,15 +307,9 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
   SplitFn split_fn = pick_split(D, G, mask_kind, ppt, nt, f != nullptr);
   CombineFn comb_fn = pick_combine(D, G);
   if (split_fn == nullptr || comb_fn == nullptr) return BZ_ERR_UNSUPPORTED;
-  bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
-  if (!two_kernels && splits > 1) {
-    int cus = 0;
-    long long resident = 0;
-    rc = device_cus(&cus);
-    if (rc == BZ_OK) rc = resident_workgroups(split_fn, nt, cus, &resident);
-    if (rc != BZ_OK) return rc;
-    two_kernels = (long long)splits * NKV * R > resident;
-  }
+  // One launch needs no residency of the whole grid: no workgroup waits for another (the last to count in merges,
+  // the others leave), so grids larger than the device runs at once merge in the same launch.
+  const bool two_kernels = a->combine == BZ_COMBINE_KERNEL;
 
   Params p = base_params(a, seq_lens, kv_start);
   p.splits = splits;

@@ -50,12 +50,13 @@ EXPORTS = (
 
 
 def source_id() -> str:
-    """Hash of what the library is built from: the translation units, their headers, the C ABI headers and the hipcc
-    flags (sha256, first 16 hex digits). build() compiles it into the library (bz_gqa_decode_build_id) and load()
-    refuses a library whose id differs from the sources next to it, as the reference's loader rebuilds when a source
-    or a flag changes (flash/kernels.py:1-4, :64-79)."""
+    """Hash of what build() compiles: the translation units, their headers, the C ABI headers, bench.py's timing
+    helper (built in the same step) and the hipcc flags (sha256, first 16 hex digits). build() compiles it into the
+    library (bz_gqa_decode_build_id) and load() refuses a library whose id differs from the sources next to it, as the
+    reference's loader rebuilds when a source or a flag changes (flash/kernels.py:1-4, :64-79); a change to the
+    timing helper's source without a rebuild is caught the same way."""
     h = hashlib.sha256()
-    files = [CSRC / f for f in SOURCES + HEADERS] + sorted(INCLUDE.glob("*.h"))
+    files = [CSRC / f for f in SOURCES + HEADERS + [STAMP_SOURCE]] + sorted(INCLUDE.glob("*.h"))
     for f in files:
         h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
     h.update(" ".join(HIPCC_FLAGS).encode())

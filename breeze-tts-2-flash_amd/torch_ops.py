@@ -4,12 +4,14 @@ pybind extension (flash/csrc/bb_attn.cu:462-469, bb_fused.cu:370-377); here the 
 operator's implementation is the package function's own call through it.
 
 Each operator writes its outputs in place (declared as mutable arguments in its schema) and returns nothing; the fake
-implementations (shapes only) do nothing, as the outputs are the caller's tensors. bz::gqa_decode and
-bz::gqa_decode_masked without a workspace run on the library's static scratch (bz_gqa_decode_noalloc), so that a
-compiled graph allocates nothing inside torch.compile's CUDA-graph trees; bz::gqa_decode_fused has no such form and
-takes the stream's cached workspace, so under CUDA-graph trees pass it a workspace allocated beforehand. The package
-functions (attention.gqa_decode and the rest) call these operators while torch.compile traces them and call the C ABI
-directly otherwise, which keeps the eager per-call host cost of a plain function call.
+implementations (shapes only) do nothing, as the outputs are the caller's tensors. Workspaces follow the package
+functions: without one, a call takes its stream's cached workspace (allocated, when first needed, outside any graph
+memory pool), except while the stream is being captured, as when torch.compile's CUDA-graph trees record a graph:
+bz::gqa_decode and bz::gqa_decode_masked then run on the library's static scratch (bz_gqa_decode_noalloc) and
+bz::gqa_decode_fused raises unless it is given a workspace made beforehand. So compiled calls on different streams
+never share a workspace. The package functions (attention.gqa_decode and the rest) call these operators while
+torch.compile traces them and call the C ABI directly otherwise, which keeps the eager per-call host cost of a plain
+function call.
 
 The operators are defined with torch.library.Library (a schema, a CUDA kernel and a fake kernel each) rather than the
 torch.library.custom_op decorator: an eager call then goes through the dispatcher straight to the kernel, without the
@@ -36,6 +38,8 @@ _SCHEMAS = {
                         "Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor cache_pos, float scale, Tensor(c!) out, "
                         "Tensor? seq_lens, Tensor? kv_start, Tensor? mask, SymInt num_splits, SymInt max_seq_len, "
                         "SymInt combine, Tensor(d!)? workspace) -> ()",
+    "gqa_decode_probs": "(Tensor q, Tensor k_cache, Tensor? seq_lens, float scale, Tensor(a!) probs, Tensor? kv_start, "
+                        "Tensor? mask) -> ()",
     "gemv_seg": "(Tensor x, Tensor? nw, float eps, Tensor W0, Tensor? W1, Tensor? W2, Tensor(a!) y) -> ()",
     "gemv_resid": "(Tensor x, Tensor W, Tensor res, Tensor(a!) y) -> ()",
     "gemv_gateup": "(Tensor x, Tensor nw, float eps, Tensor Wg, Tensor Wu, Tensor(a!) y) -> ()",
@@ -46,7 +50,7 @@ _SCHEMAS = {
 def _gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_splits, max_seq_len, combine,
                 workspace):
     attention._gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_splits, max_seq_len, combine,
-                          workspace, static_scratch=True)
+                          workspace)
 
 
 def _gqa_decode_wave(q, k_cache, v_cache, seq_lens, scale, out, kv_start):
@@ -54,14 +58,17 @@ def _gqa_decode_wave(q, k_cache, v_cache, seq_lens, scale, out, kv_start):
 
 
 def _gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine, workspace):
-    attention._gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine, workspace,
-                                 static_scratch=True)
+    attention._gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine, workspace)
 
 
 def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
                       seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace):
     attention._gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale,
                                 out, seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace)
+
+
+def _gqa_decode_probs(q, k_cache, seq_lens, scale, probs, kv_start, mask):
+    attention._gqa_decode_probs(q, k_cache, seq_lens, scale, probs, kv_start, mask)
 
 
 # the GEMV bodies return their output tensor; an operator whose schema returns () must return None
@@ -86,6 +93,7 @@ _KERNELS = {
     "gqa_decode_wave": _gqa_decode_wave,
     "gqa_decode_masked": _gqa_decode_masked,
     "gqa_decode_fused": _gqa_decode_fused,
+    "gqa_decode_probs": _gqa_decode_probs,
     "gemv_seg": _gemv_seg,
     "gemv_resid": _gemv_resid,
     "gemv_gateup": _gemv_gateup,

@@ -111,3 +111,51 @@ def test_opcheck(device, op):
         res = torch.randn(2, 256, generator=gen, device=device).bfloat16()
         y = torch.empty(2, 256, dtype=torch.bfloat16, device=device)
         torch.library.opcheck(torch.ops.bz.gemv_resid.default, (x, W, res, y))
+
+
+def test_compiled_calls_on_two_streams(device):
+    """Compiled calls (default mode) issued on two streams at once, without synchronising between them: each stream's
+    calls take that stream's own cached workspace, so calls in flight together share no arrival counters or partials,
+    and every output equals the eager call bit for bit."""
+    cases = [rand_case(95 + i, 2, 16, 8, 128, 2048, [2000 - 300 * i, 1500 + 200 * i], [0, 3 * i]) for i in range(2)]
+    gs = [(w.to(device), st.to(device)) for w, st in cases]
+
+    def step(q, k, v, lens, kv_start, out):
+        gqa_decode(q, k, v, lens, cases[0][0].scale, out, kv_start=kv_start)
+        return out
+
+    refs = [gqa_decode(g.q, g.k, g.v, g.seq_lens, cases[0][0].scale, kv_start=st) for g, st in gs]
+    torch._dynamo.reset()
+    compiled = torch.compile(step, fullgraph=True)
+    outs = [torch.empty_like(r) for r in refs]
+    streams = [torch.cuda.Stream(device) for _ in range(2)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(device))
+    for it in range(30):
+        for i, (g, st) in enumerate(gs):
+            with torch.cuda.stream(streams[i]):
+                compiled(g.q, g.k, g.v, g.seq_lens, st, outs[i])
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(_bits(outs[i]), _bits(refs[i])), f"stream {i}"
+
+
+def test_compiled_attention_cudagraph_trees(device):
+    """torch.compile(mode="reduce-overhead"): CUDA-graph trees warm the function up eagerly, record it into a graph,
+    then replay it. The warm-up takes a stream workspace allocated outside the trees' memory pool (which must hold
+    only the graph's outputs), the recording runs on the library's static scratch, and every call equals the eager
+    result bit for bit."""
+    w, st = rand_case(96, 2, 16, 8, 128, 2048, [1024, 1024])
+    g = w.to(device)
+
+    def step(q, k, v, lens):
+        return gqa_decode(q, k, v, lens, w.scale)
+
+    ref = step(g.q, g.k, g.v, g.seq_lens)
+    torch._dynamo.reset()
+    compiled = torch.compile(step, mode="reduce-overhead", fullgraph=True)
+    for i in range(5):
+        got = compiled(g.q, g.k, g.v, g.seq_lens).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(got), _bits(ref)), f"call {i}"
+    torch._dynamo.reset()

@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from breeze_tts_2_flash_amd import attn_decode_fused, gqa_decode_fused
+from breeze_tts_2_flash_amd.attention import get_workspace
 from oracle.attention import fused_decode, interval_mask, rope_cos_sin
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
 
@@ -131,9 +132,11 @@ def test_fused_decode_loop_in_hip_graph(device):
     cp = torch.tensor([100], dtype=torch.int64, device=device)
     lens = torch.tensor([101, 101], dtype=torch.int32, device=device)
     out = torch.empty(B, 16, D, dtype=torch.bfloat16, device=device)
+    # a captured fused call needs its workspace made beforehand (nothing is allocated during a capture)
+    ws = get_workspace(device, B, 16, 8, D, 256)
     call = lambda: gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc, vc, cp, D ** -0.5, out,  # noqa: E731
-                                    seq_lens=lens)
-    call()  # eager step at slot 100 (allocates the workspace outside capture)
+                                    seq_lens=lens, workspace=ws)
+    call()  # eager step at slot 100
     torch.cuda.synchronize()
     ref_k, ref_v = s["kc"], s["vc"]
     _, ref_k, ref_v = fused_decode(s["qkv"], s["qn"], s["kn"], 1e-6, s["cos"], s["sin"], ref_k, ref_v, 100,

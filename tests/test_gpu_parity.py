@@ -436,14 +436,16 @@ def test_concurrent_streams_and_threads(device):
         assert_close(outs[i], oracle(cases[i][0]), f"stream {i}")
 
 
-@pytest.mark.parametrize("splits", [0, 1, 7, 256])
-def test_long_context(device, splits):
+@pytest.mark.parametrize("splits,combine", [(0, "auto"), (1, "auto"), (7, "auto"), (256, "auto"), (256, "last_block")])
+def test_long_context(device, splits, combine):
     """A 32768-slot cache: a full row and a left-padded partial one, the default split count (chunks capped at 256
     positions), one workgroup streaming 32768 positions in 512 tiles, a ragged 7-way split, and the largest split
-    count (256)."""
+    count (256). At 256 splits the grid is 2 x 8 x 256 = 4096 workgroups, more than the GPU holds at once (256 CUs,
+    at most 5 of these workgroups each), and the splits are still merged inside the one launch: no workgroup waits for
+    another, the last of each (row, kv head) to count in merges."""
     lens, starts = [32768, 20001], [0, 5]
     w, st = rand_case(31 + splits, 2, 16, 8, 128, 32768, lens, starts)
     g = w.to(device)
-    out = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=splits)
+    out = gqa_decode(g.q, g.k, g.v, g.seq_lens, g.scale, kv_start=st.to(device), num_splits=splits, combine=combine)
     torch.cuda.synchronize()
-    assert_close(out.float().cpu(), oracle(w, kv_start=st), f"long context splits={splits}")
+    assert_close(out.float().cpu(), oracle(w, kv_start=st), f"long context splits={splits} combine={combine}")

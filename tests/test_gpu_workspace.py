@@ -133,3 +133,143 @@ def test_capture_without_workspace_allocates_nothing(device):
         assert torch.equal(out_m.view(torch.int16), ref_m.view(torch.int16)), f"replay {i} (masked)"
         again = gqa_decode(g.q[:1], g.k[:1], g.v[:1], g.seq_lens[:1], g.scale, num_splits=8)
         assert torch.equal(again.view(torch.int16), small.view(torch.int16)), f"eager call after replay {i}"
+
+
+def _step_inputs(device, B=2, NH=16, NKV=8, D=128, cap=1024, L=700, seed=81):
+    """Raw q | k | v projections, norm weights, RoPE tables, caches and the cache slot of one fused decode step."""
+    gen = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(B, (NH + 2 * NKV) * D, generator=gen) * 2).bfloat16().to(device)
+    qn = (1 + 0.2 * torch.randn(D, generator=gen)).bfloat16().to(device)
+    kn = (1 + 0.2 * torch.randn(D, generator=gen)).bfloat16().to(device)
+    ang = torch.linspace(0, 3, D)
+    cos = ang.cos().bfloat16().expand(B, D).contiguous().to(device)
+    sin = ang.sin().bfloat16().expand(B, D).contiguous().to(device)
+    kc = torch.randn(B, NKV, cap, D, generator=gen).bfloat16().to(device)
+    vc = torch.randn(B, NKV, cap, D, generator=gen).bfloat16().to(device)
+    pos = torch.tensor([L - 1], dtype=torch.int64, device=device)
+    lens = torch.full((B,), L, dtype=torch.int32, device=device)
+    return qkv, qn, kn, cos, sin, kc, vc, pos, lens
+
+
+def test_fused_capture_allocates_nothing(device):
+    """The fused entry under capture: without workspace= it raises before launching anything (it has no static-scratch
+    form, and a capture must not allocate); with a workspace made before the capture it records, allocates nothing,
+    and every replay equals the eager step bit for bit (caches included)."""
+    qkv, qn, kn, cos, sin, kc0, vc0, pos, lens = _step_inputs(device)
+    kc, vc = kc0.clone(), vc0.clone()
+    ref = gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc, vc, pos, 128 ** -0.5, seq_lens=lens)
+    torch.cuda.synchronize()
+    ref_k, ref_v = kc.clone(), vc.clone()
+    ws = attention.get_workspace(device, 2, 16, 8, 128, 1024)
+    out = torch.empty_like(ref)
+    keys = set(attention._WS)
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="workspace"):
+            with torch.cuda.graph(graph, stream=side):
+                gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc2, vc2, pos, 128 ** -0.5, out, seq_lens=lens)
+        torch.cuda.synchronize()
+        assert set(attention._WS) == keys, "the refused capture allocated a workspace"
+        before = torch.cuda.memory_allocated(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc2, vc2, pos, 128 ** -0.5, out, seq_lens=lens,
+                             workspace=ws)
+        assert torch.cuda.memory_allocated(device) == before, "the capture allocated device memory"
+    assert set(attention._WS) == keys, "the capture added a cached workspace"
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+        assert torch.equal(kc2.view(torch.int16), ref_k.view(torch.int16)), f"replay {i}: k cache"
+        assert torch.equal(vc2.view(torch.int16), ref_v.view(torch.int16)), f"replay {i}: v cache"
+        _counters_clear(ws, 2 * 8, f"replay {i}")
+
+
+def test_reference_fused_entry_capture_allocates_nothing(device):
+    """compat.attn_decode_fused, the entry the reference's decode step calls (flash/backbone.py:123-124), in the
+    reference's capture sequence (backbone_graph.py:288-315): eager warm-up calls with the reference's workspaces, then
+    a capture on a side stream. The capture allocates nothing (the warm-up made the library workspace this call's
+    `counters` buffer keys) and every replay equals the eager step; a capture with a `counters` buffer never seen
+    eagerly raises instead of allocating."""
+    from breeze_tts_2_flash_amd import compat
+
+    qkv, qn, kn, cos, sin, kc0, vc0, pos, lens = _step_inputs(device, seed=82)
+    B, NH, NKV, D, cap, L = 2, 16, 8, 128, 1024, 700
+    mask = interval_mask([0, 0], L - 1, cap).to(device)
+    scores = torch.empty(B, NH, cap, device=device)
+    cmax = torch.empty(B, NH, cap // 64, device=device)
+    part = torch.empty(B, NH, cap // 64, D, device=device)
+    counters = torch.zeros(B, NKV, 4, dtype=torch.int32, device=device)
+    kc, vc = kc0.clone(), vc0.clone()
+    ref = torch.empty(B, 1, NH, D, dtype=torch.bfloat16, device=device)
+    for _ in range(3):  # the reference's warm-up steps
+        kc.copy_(kc0)
+        vc.copy_(vc0)
+        compat.attn_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc, vc, mask, pos, D ** -0.5, scores, cmax, part,
+                                 counters, ref)
+    torch.cuda.synchronize()
+    ref_k, ref_v = kc.clone(), vc.clone()
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    out = torch.empty_like(ref)
+    ws_keys, lib_keys = set(compat._WS), set(attention._WS)
+    before = torch.cuda.memory_allocated(device)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            compat.attn_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc2, vc2, mask, pos, D ** -0.5, scores, cmax, part,
+                                     counters, out)
+        other = torch.zeros_like(counters)
+        with pytest.raises(RuntimeError, match="eagerly"):
+            with torch.cuda.graph(torch.cuda.CUDAGraph(), stream=side):
+                compat.attn_decode_fused(qkv, qn, kn, 1e-6, cos, sin, kc2, vc2, mask, pos, D ** -0.5, scores, cmax,
+                                         part, other, out)
+    torch.cuda.synchronize()
+    del other
+    assert set(compat._WS) == ws_keys and set(attention._WS) == lib_keys, "the captures added a workspace"
+    assert torch.cuda.memory_allocated(device) == before, "the captures allocated device memory"
+    for i in range(3):
+        out.zero_()
+        kc2.copy_(kc0)
+        vc2.copy_(vc0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+        assert torch.equal(kc2.view(torch.int16), ref_k.view(torch.int16)), f"replay {i}: k cache"
+        assert torch.equal(vc2.view(torch.int16), ref_v.view(torch.int16)), f"replay {i}: v cache"
+
+
+def test_capture_beyond_the_static_scratch_raises(device):
+    """A non-fused call captured without workspace= whose sizes exceed the static scratch (more than 1024 (row, kv
+    head) groups) raises rather than allocate a workspace inside the capture; with workspace= it records."""
+    B, NH, NKV, D, cap = 160, 16, 8, 64, 128  # 1280 groups
+    gen = torch.Generator().manual_seed(83)
+    q = torch.randn(B, NH, D, generator=gen).bfloat16().to(device)
+    k = torch.randn(B, NKV, cap, D, generator=gen).bfloat16().to(device)
+    v = torch.randn(B, NKV, cap, D, generator=gen).bfloat16().to(device)
+    lens = torch.full((B,), cap, dtype=torch.int32, device=device)
+    ref = gqa_decode(q, k, v, lens, D ** -0.5, num_splits=2)
+    ws = attention.get_workspace(device, B, NH, NKV, D, cap, 2)
+    out = torch.empty_like(ref)
+    keys = set(attention._WS)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        with pytest.raises(RuntimeError, match="SCRATCH|scratch"):
+            with torch.cuda.graph(torch.cuda.CUDAGraph(), stream=side):
+                gqa_decode(q, k, v, lens, D ** -0.5, out, num_splits=2)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            gqa_decode(q, k, v, lens, D ** -0.5, out, num_splits=2, workspace=ws)
+    assert set(attention._WS) == keys, "a capture added a cached workspace"
+    for i in range(2):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"

@@ -17,6 +17,7 @@ WRITES = {
     "gqa_decode_wave": {"out"},
     "gqa_decode_masked": {"out", "workspace"},
     "gqa_decode_fused": {"k_cache", "v_cache", "out", "workspace"},
+    "gqa_decode_probs": {"probs"},
     "gemv_seg": {"y"},
     "gemv_resid": {"y"},
     "gemv_gateup": {"y"},
