@@ -442,20 +442,19 @@ GemvFn pick_r(int r, int epi, bool norm, bool pace) {
   }
 }
 
-// x in registers for m * chunks <= 8 with m <= 2 (KC = 4: k <= 2048) or m <= 4 (KC = 2: k <= 1024); LDS otherwise.
+// x in registers for k <= 2048 (KC = 2: k <= 1024, KC = 4: k <= 2048); LDS otherwise.
 template <int M>
 GemvFn pick_kc(int kc, int r, int epi, bool norm, bool pace) {
-  if constexpr (M <= 2) {
-    if (kc == 4) return pick_r<M, 4>(r, epi, norm, pace);
-  }
+  if (kc == 4) return pick_r<M, 4>(r, epi, norm, pace);
   if (kc == 2) return pick_r<M, 2>(r, epi, norm, pace);
   return pick_r<M, 0>(r, epi, norm, pace);
 }
 
 // Chunks of x per lane held in registers (0: x in LDS).
 int kc_for(int m, int k) {
+  (void)m;
   const int chunks = (k + kChunk - 1) / kChunk;
-  return chunks <= 2 ? 2 : (chunks <= 4 && m <= 2 ? 4 : 0);
+  return chunks <= 2 ? 2 : (chunks <= 4 ? 4 : 0);
 }
 
 GemvFn pick_gemv(int m, int kc, int r, int epi, bool norm, bool pace) {
