@@ -275,11 +275,12 @@ BACKBONE_GEMV_BYTES = {"gemv_qkv_norm_bytes": 2 * 4096 * 2048, "gemv_o_resid_byt
                        "gemv_gateup_norm_silu_bytes": 2 * 2 * 6144 * 2048, "gemv_down_resid_bytes": 2 * 2048 * 6144}
 
 
-def per_call_times(pkg, w, dev, calls):
-    """The distribution of single cold calls of workload w: one HIP graph holding a GPU stamp before every call (and
-    one after the last), rotating over ROTATE_BYTES of K/V sets, replayed twice after a cache flush; each interval
-    between stamps is one stamp launch plus one call, and the median interval of a graph of stamps alone is
-    subtracted. Returns a dict of µs figures (mean, percentiles, a 0.25 µs histogram)."""
+def per_call_times(pkg, w, dev, calls, fused=False):
+    """The distribution of single cold calls of workload w (fused: fused decode steps, as time_calls makes them): one
+    HIP graph holding a GPU stamp before every call (and one after the last), rotating over ROTATE_BYTES of K/V sets,
+    replayed twice after a cache flush; each interval between stamps is one stamp launch plus one call, and the
+    median interval of a graph of stamps alone is subtracted. Returns a dict of µs figures (mean, percentiles, a
+    0.25 µs histogram)."""
     import numpy as np
     import torch
     from breeze_tts_2_flash_amd import workloads
@@ -293,9 +294,17 @@ def per_call_times(pkg, w, dev, calls):
     vs.copy_(g.v.expand_as(vs))
     out = torch.empty(w.batch, w.num_q_heads, w.head_dim, dtype=torch.bfloat16, device=dev)
 
+    if fused:
+        qkv, qn, kn, cos, sin, cache_pos = fused_inputs(w, dev)
+        ws = pkg.get_workspace(dev, w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.capacity)
+
     def call(i):  # sets 0 and 1 for the two lead calls, then 2 .. nsets - 1 in turn
         j = 2 + i % (nsets - 2) if i >= 0 else i + 2
-        pkg.gqa_decode(g.q, ks[j], vs[j], g.seq_lens, g.scale, out)
+        if fused:
+            pkg.gqa_decode_fused(qkv, qn, kn, 1e-6, cos, sin, ks[j], vs[j], cache_pos, g.scale, out,
+                                 seq_lens=g.seq_lens, workspace=ws)
+        else:
+            pkg.gqa_decode(g.q, ks[j], vs[j], g.seq_lens, g.scale, out)
 
     def intervals(body, flush):
         st = GpuStamps(dev, n=calls + 1)
@@ -700,8 +709,8 @@ def main():
         return
     cfg = args.config
     if args.per_call:
-        print(json.dumps({"per_call_us": per_call_times(pkg, workloads.make(cfg), dev, args.per_call),
-                          "config": cfg}), flush=True)
+        print(json.dumps({"per_call_us": per_call_times(pkg, workloads.make(cfg), dev, args.per_call, args.fused),
+                          "config": cfg, "fused": args.fused}), flush=True)
         return
     w2 = workloads.make(cfg)
     splits2 = args.splits or pkg.default_splits(w2.batch, w2.num_kv_heads, w2.head_dim, w2.capacity, 0)
