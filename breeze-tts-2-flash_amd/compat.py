@@ -39,7 +39,7 @@ def _fused_workspace(qkv: torch.Tensor, kc: torch.Tensor, NH: int, counters) -> 
         raise RuntimeError("attn_decode_fused: no workspace exists yet for these sizes, and nothing is allocated during "
                            "a capture: run the decode step once eagerly before capturing it (as BackboneGraph.capture "
                            "does)")
-    ws = torch.zeros((need + 255) // 256 * 256, dtype=torch.uint8, device=qkv.device)
+    ws = attention._zeroed_outside_pools((need + 255) // 256 * 256, idx)
     if ws.data_ptr() % 256:
         raise RuntimeError("workspace allocation is not 256-byte aligned")
     _WS[key] = ws
