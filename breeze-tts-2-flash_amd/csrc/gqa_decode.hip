@@ -341,7 +341,7 @@ int launch(const bz_gqa_decode_args* a, hipStream_t stream, const int32_t* seq_l
     p.v_out = const_cast<uint16_t*>(p.v);
   }
 
-  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, R), dim3(nt), 0, stream, p.seq_lens, p.kv_start, p);
+  hipLaunchKernelGGL(split_fn, dim3(splits, NKV, R), dim3(nt), 0, stream, p.seq_lens, p.kv_start, p.T, p);
   if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
   if (two_kernels && splits > 1) {
     hipLaunchKernelGGL(comb_fn, dim3(NKV, R), dim3(kThreads), 0, stream, p);

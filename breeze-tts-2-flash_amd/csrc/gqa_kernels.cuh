@@ -73,11 +73,12 @@ struct Params {
 };
 
 // The split kernels take the rows' range arrays (seq_lens, kv_start) as leading kernel arguments ahead of the
-// parameter block: built with kernel-argument preloading (-mllvm -amdgpu-kernarg-preload-count), the leading scalar
-// arguments of a kernel (up to 56 bytes; a struct argument is never preloaded) arrive in SGPRs with the wave, so the
-// range loads go out at once instead of after a load of the argument buffer. Without preloading they are read from
-// the argument buffer like the rest.
-using SplitFn = void (*)(const int32_t*, const int32_t*, const Params);
+// parameter block, and so does the number of query tokens per row, which the row index (and so the address of its
+// range) depends on: built with kernel-argument preloading (-mllvm -amdgpu-kernarg-preload-count), the leading
+// scalar arguments of a kernel (up to 56 bytes; a struct argument is never preloaded) arrive in SGPRs with the wave,
+// so the range loads go out at once, together with the loads of the argument buffer rather than after one. Without
+// preloading they are read from the argument buffer like the rest.
+using SplitFn = void (*)(const int32_t*, const int32_t*, int, const Params);
 using CombineFn = void (*)(const Params);
 
 // Kernel tables (gqa_fused.hip defines the fused one).
@@ -223,7 +224,8 @@ __device__ __forceinline__ void st_agent(float* ptr, float v) {
   __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output.
+// Merge the nact split partials of the G q heads of kv head h in split order and write the bf16 output. tpr: query
+// tokens per row (p.T; the split kernel has it in an SGPR from the launch, so a row index needs no division at T = 1).
 // The partials of one (row, kv head) are read through buffer resources cut at nact splits, with the sc1 cache policy
 // (bit 4 of the buffer instruction's cache-policy operand on gfx940 and later: the cache behaviour of an agent-scope
 // relaxed atomic load), so every load is unconditional and splits past nact read 0 without a memory access. All loads
@@ -234,7 +236,7 @@ __device__ __forceinline__ void st_agent(float* ptr, float v) {
 // start at zero (clearing the partials as well, so that the whole workspace is zero between calls, cost 0.26 us per
 // call at the serving shape and 0.5 us on the ragged batch).
 template <int D, int G, int NT>
-__device__ void merge_splits(const Params& p, int z, int h, int nact) {
+__device__ void merge_splits(const Params& p, int z, int h, int nact, int tpr) {
   constexpr int kBatch = 16;
   constexpr int NW = NT / kWave;
   constexpr int kOut = (G * D + NT - 1) / NT;
@@ -245,7 +247,7 @@ __device__ void merge_splits(const Params& p, int z, int h, int nact) {
   const int64_t unit = (int64_t)z * p.NKV + h;
   const Rsrc racc = span_rsrc(p.part_acc + unit * p.splits * GD, nact * GD * 4);
   const Rsrc rml = span_rsrc(p.part_ml + unit * p.splits * G, nact * G * 8);
-  const int b = z / p.T, tok = z - b * p.T;
+  const int b = tpr == 1 ? z : z / tpr, tok = z - b * tpr;
   uint16_t* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)tok * p.o_st;
 
   // The (max, sum) pairs of q head wave % G first, by every wave and without a condition (a wave past the group's
@@ -540,7 +542,8 @@ __device__ __forceinline__ void consume_tile(Tile<PPT>& t, const uint4 (&qp)[G],
 
 // lens, starts: p.seq_lens and p.kv_start again, as leading (preloaded) arguments.
 template <int D, int G, int PPT, int MK, int NT, bool FUSED>
-__global__ void __launch_bounds__(NT) gqa_split_kernel(const int32_t* lens, const int32_t* starts, const Params p) {
+__global__ void __launch_bounds__(NT) gqa_split_kernel(const int32_t* lens, const int32_t* starts, const int tpr,
+                                                       const Params p) {
   constexpr int NW = NT / kWave;        // waves per workgroup
   constexpr int LPR = D / 8;            // lanes per KV row, 16 B (8 bf16) each
   constexpr int ROWS = NT / LPR;        // KV rows per load instruction across the workgroup
@@ -549,7 +552,8 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const int32_t* lens, cons
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
 
   const int split = blockIdx.x, h = blockIdx.y, z = blockIdx.z;  // z = row * T + token
-  const int b = p.T == 1 ? z : z / p.T, tok = z - b * p.T;  // T = 1 but in the depth step's two-token first step
+  // tpr = p.T, preloaded: T = 1 but in the depth step's two-token first step
+  const int b = tpr == 1 ? z : z / tpr, tok = z - b * tpr;
   const int tid = threadIdx.x, c = tid % LPR, r = tid / LPR;
 
   // q of the G heads of this group, this lane's 8 dims, issued first, since none of it depends on the row's length.
@@ -566,7 +570,8 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const int32_t* lens, cons
   // The row's length and start first, ahead of every vector load of the workgroup: the CU's vector memory queue is
   // shared with the workgroups already streaming there (four per CU on a 1024-workgroup grid), and a q load waiting
   // for room in it would hold up these scalar loads behind it in program order. Their addresses come from the
-  // preloaded leading arguments, so the loads do not wait for the argument buffer.
+  // preloaded leading arguments (the range arrays, and the token count that gives the row index), so the loads go
+  // out together with those of the argument buffer instead of one round trip after them.
   int e_raw = 0, s_raw = 0;
   if (MK == BZ_MASK_NONE) {
     e_raw = lens[b];
@@ -776,7 +781,7 @@ __global__ void __launch_bounds__(NT) gqa_split_kernel(const int32_t* lens, cons
   }
   __syncthreads();
   if (!s_last) return;
-  merge_splits<D, G, NT>(p, z, h, nact);
+  merge_splits<D, G, NT>(p, z, h, nact, tpr);
 }
 
 // Second-launch merge: one workgroup per (kv head, row).
@@ -788,7 +793,7 @@ __global__ void __launch_bounds__(kThreads) gqa_combine_kernel(const Params p) {
   const int len = end - start;
   const int nact = split_count(len, split_chunk<D>(len, p.splits, p.inv_splits, p.min_chunk));
   if (nact == 1) return;  // the split kernel wrote the output
-  merge_splits<D, G, kThreads>(p, z, h, nact);
+  merge_splits<D, G, kThreads>(p, z, h, nact, p.T);
 }
 
 // Interval of the additive mask row: first and last position with value > -1e30.
