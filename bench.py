@@ -23,6 +23,7 @@ models/breeze.py:259-286, as restated in oracle/attention.py:eager_bf16) on the 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -53,6 +54,9 @@ def parse_args():
                    help="rows of the --backbone-only step (default 2, the CFG pair)")
     p.add_argument("--depth-only", action="store_true",
                    help="only the depth frames: config 5 (split and wave kernels) and the real depth shape")
+    p.add_argument("--protocol-only", action="store_true",
+                   help="only the protocol floor: the split kernel's K/V traffic without arithmetic, with and without "
+                        "its exchange, configs 2-4, beside the kernel's own cold time")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--per-call", type=int, default=0, metavar="N",
                    help="only the distribution of N single cold calls of --config (a GPU stamp before every call)")
@@ -383,6 +387,87 @@ def time_stream_floor(dev, sizes):
     return out
 
 
+class KvPatternArgs(ctypes.Structure):
+    """bz_bench_kv_args of libbz_bench_stamp.so."""
+    _fields_ = [("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p), ("kv_stride_b", ctypes.c_int64),
+                ("kv_stride_h", ctypes.c_int64), ("kv_stride_s", ctypes.c_int64), ("seq_lens", ctypes.c_void_p),
+                ("rows", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("capacity", ctypes.c_int32), ("splits", ctypes.c_int32), ("exchange", ctypes.c_int32),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t), ("out", ctypes.c_void_p),
+                ("sink", ctypes.c_void_p)]
+
+
+def _pattern_chunks(length, splits, D=128):
+    """The split kernel's chunk count for a row of `length` positions (min chunk 16 KB of K+V, one split up to
+    64 KB), which is what bz_bench_kv_pattern writes for the row when it exchanges."""
+    min_chunk, one = 16 * 1024 // (4 * D), 64 * 1024 // (4 * D)
+    if length <= 0:
+        return 1
+    chunk = max(length, min_chunk) if length <= one else max(-(-length // splits), min_chunk)
+    return -(-length // chunk)
+
+
+def time_protocol_floor(pkg, dev, configs=(2, 3, 4)):
+    """The floor the split kernel's own traffic and exchange set, per config: µs per launch of bz_bench_kv_pattern
+    (the kernel's grid, chunk rule and K/V loads with no arithmetic), without and with the kernel's exchange protocol,
+    timed exactly as the cold calls (EXTRA_CALLS launches in one HIP graph between GPU stamps, 2 untimed lead launches,
+    rotating over ROTATE_BYTES of K/V sets, after a flush). Each output is checked against the rows' chunk counts
+    (every (row, kv head) merged once). Returns {configN: {"splits", "pattern_us", "pattern_exchange_us"}}."""
+    import torch
+    from breeze_tts_2_flash_amd import workloads
+
+    lib = GpuStamps.library()
+    lib.bz_bench_kv_pattern.argtypes = [ctypes.POINTER(KvPatternArgs), ctypes.c_void_p]
+    lib.bz_bench_kv_pattern_workspace.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                                  ctypes.POINTER(ctypes.c_size_t)]
+    res = {}
+    for xc in configs:
+        w = workloads.make(xc)
+        B, NKV, D, cap = w.batch, w.num_kv_heads, w.head_dim, w.capacity
+        splits = pkg.default_splits(B, NKV, D, cap, 0)
+        lens = w.seq_lens.tolist()
+        read_bytes = workloads.algorithmic_bytes(lens, w.num_q_heads, NKV, D)
+        nsets = max(16, math.ceil(ROTATE_BYTES / read_bytes)) + 2
+        ks = torch.empty((nsets,) + tuple(w.k.shape), dtype=torch.bfloat16, device=dev)
+        vs = torch.empty_like(ks)
+        ks.copy_(w.k.to(dev).expand_as(ks))
+        vs.copy_(w.v.to(dev).expand_as(vs))
+        seq = w.seq_lens.to(dev)
+        nbytes = ctypes.c_size_t(0)
+        if lib.bz_bench_kv_pattern_workspace(B, NKV, splits, ctypes.byref(nbytes)) != 0:
+            raise RuntimeError("bz_bench_kv_pattern_workspace failed")
+        ws = torch.zeros(nbytes.value, dtype=torch.uint8, device=dev)
+        out = torch.zeros(B * NKV * 256, dtype=torch.int16, device=dev)
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        entry = {"splits": splits}
+        for exchange in (0, 1):
+            a = KvPatternArgs(None, None, ks.stride(1), ks.stride(2), ks.stride(3), seq.data_ptr(), B, NKV, D, cap,
+                              splits, exchange, ws.data_ptr(), nbytes.value, out.data_ptr(), sink.data_ptr())
+
+            def launch(j):
+                a.k_cache, a.v_cache = ks[j].data_ptr(), vs[j].data_ptr()
+                if lib.bz_bench_kv_pattern(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)):
+                    raise RuntimeError("bz_bench_kv_pattern failed")
+
+            def lead():
+                launch(0)
+                launch(1)
+
+            def timed():
+                for i in range(EXTRA_CALLS):
+                    launch(2 + i % (nsets - 2))
+            us = time_captured(capture_timed(timed, dev, lead=lead), dev) / EXTRA_CALLS
+            want = torch.tensor([_pattern_chunks(n, splits, D) if exchange else 1 for n in lens for _ in range(NKV)],
+                                dtype=torch.float32).repeat_interleave(256).bfloat16().view(torch.int16)
+            if not torch.equal(out.cpu(), want):
+                raise RuntimeError(f"bz_bench_kv_pattern (config {xc}, exchange {exchange}): wrong chunk counts")
+            entry["pattern_exchange_us" if exchange else "pattern_us"] = round(us, 3)
+        res[f"config{xc}"] = entry
+        del ks, vs
+        torch.cuda.empty_cache()
+    return res
+
+
 def make_backbone(dev, M=2):
     """Random-init weights, KV caches and buffers of the reference's backbone at its serving shape (a Qwen3 of hidden
     2048, 16 q / 8 KV heads of 128, intermediate 6144, 28 layers; KV 1024 of 2048 slots) for M rows: 2 is the CFG
@@ -699,6 +784,13 @@ def main():
         bb = {f"m{M}": time_backbone(pkg, dev, M=M) for M in args.backbone_m}
         print(json.dumps({"backbone": bb}), flush=True)
         return
+    if args.protocol_only:
+        floor = time_protocol_floor(pkg, dev)
+        for xc in (2, 3, 4):
+            floor[f"config{xc}"]["kernel_us"] = round(
+                time_calls(pkg, workloads.make(xc), dev, EXTRA_CALLS, args.warmup, "auto", 0, False, cold=True)[0], 3)
+        print(json.dumps({"protocol_floor": floor}), flush=True)
+        return
     if args.depth_only:
         us_f, _ = time_depth_frame(pkg, dev)
         us_w, _ = time_depth_frame(pkg, dev, wave=True)
@@ -780,6 +872,17 @@ def main():
                            "algorithmic bytes and the backbone GEMVs' weight bytes, timed like the cold calls; "
                            "keyed by workgroup count")
         extra["stream_floor"] = floor
+        proto = time_protocol_floor(pkg, dev)
+        for xc in (2, 3, 4):
+            kus = us if xc == cfg and not args.fused else extra.get(f"config{xc}_cold", {}).get("us_per_call")
+            if kus is not None:
+                proto[f"config{xc}"]["kernel_us"] = round(kus, 3)
+            print(f"[bench] protocol floor, config {xc}: {proto[f'config{xc}']}", file=sys.stderr, flush=True)
+        proto["method"] = ("bz_bench_kv_pattern: the split kernel's grid, chunk rule and K/V loads with no arithmetic "
+                           "(pattern_us), then also its exchange protocol on a 1 KB partial per workgroup "
+                           "(pattern_exchange_us), timed like the cold calls; kernel_us is the kernel's own cold time "
+                           "in this run")
+        extra["protocol_floor"] = proto
         us_f, fb = time_depth_frame(pkg, dev)
         extra["config5_depth_frame"] = {"us_per_frame": round(us_f, 3), "us_per_call": round(us_f / 32, 3),
                                         "bytes_per_frame": fb, "GB/s": round(fb / us_f / 1e3, 1),
