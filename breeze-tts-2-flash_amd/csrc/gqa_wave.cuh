@@ -2,7 +2,8 @@
 // persistent depth-transformer kernel of the reference's kind, flash/csrc/depth_frame.cu:193-272, whose attention
 // stage gives each warp one (row, q head) pair over at most 17 cached positions). Here too one wave owns one (row,
 // q head), and the K/V bytes go from the cache straight into VGPRs (no LDS staging, no barrier), so the caller may run
-// it from any wave of any workgroup, with other waves busy elsewhere. Any length works; it is built for short ones
+// it from any wave of any workgroup, with other waves busy elsewhere (tests/csrc/wave_stage.hip runs it so, beside
+// waves streaming a scratch buffer through LDS). Any length works; it is built for short ones
 // (two tiles of 4 * 64 / (D / 8) positions: 32 at head_dim 128).
 //
 // The q heads of a group read the same K/V bytes, each through its own wave (from the L2 after the first). A wave that
