@@ -457,11 +457,38 @@ def gqa_decode_fused(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
                              out, seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace)
 
 
-def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
-                      seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace,
-                      probs=None) -> torch.Tensor:
-    """gqa_decode_fused's call through the C ABI; with probs (float32 [B, NH, capacity]), then the step's softmax
-    probabilities into it (bz_gqa_decode_fused_probs: the reference's dbg output of attn_decode_fused)."""
+_FUSED: dict = {}  # layout of a fused call -> (checked GqaDecodeFusedArgs bytes, out shape)
+
+
+def _layout(t):
+    return None if t is None else (t.shape, t.stride(), t.dtype, t.device)
+
+
+def _fused_args(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out, seq_lens,
+                kv_start, mask, num_splits, max_seq_len, combine):
+    """The bz_gqa_decode_fused_args of a call (every pointer but the workspace's filled in) and its output tensor
+    (allocated when out is None). The checks depend only on the tensors' layout (shapes, strides, dtypes, devices) and
+    the scalars, so a layout seen before reuses its checked arguments and only the pointers are set."""
+    key = (qkv.shape, qkv.stride(), qkv.dtype, qkv.device, k_cache.shape, k_cache.stride(), k_cache.dtype,
+           k_cache.device, v_cache.shape, v_cache.stride(), v_cache.dtype, v_cache.device, _layout(q_norm_weight),
+           _layout(k_norm_weight), _layout(cos), _layout(sin), _layout(cache_pos), _layout(out), _layout(seq_lens),
+           _layout(kv_start), _layout(mask), eps, scale, num_splits, max_seq_len, combine)
+    hit = _FUSED.get(key)
+    if hit is not None:
+        f = kernels.GqaDecodeFusedArgs.from_buffer_copy(hit[0])
+        if out is None:
+            out = torch.empty(hit[1], dtype=torch.bfloat16, device=qkv.device)
+        a = f.base  # shares f's memory
+        a.q = f.qkv = qkv.data_ptr()
+        a.k_cache, a.v_cache, a.out = k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr()
+        if seq_lens is not None:
+            a.seq_lens = seq_lens.data_ptr()
+            a.kv_start = kv_start.data_ptr() if kv_start is not None else None
+        if mask is not None:
+            a.mask = mask.data_ptr()
+        f.q_norm_weight, f.k_norm_weight = q_norm_weight.data_ptr(), k_norm_weight.data_ptr()
+        f.cos, f.sin, f.cache_pos = cos.data_ptr(), sin.data_ptr(), cache_pos.data_ptr()
+        return f, out
     _check(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.dtype == torch.bfloat16,
            "qkv must be a bf16 [B, (NH + 2 NKV) * D] tensor with a contiguous last dim")
     _check(k_cache.dim() == 4, "k_cache must be [B, NKV, capacity, D]")
@@ -495,6 +522,21 @@ def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
     f.q_norm_weight, f.k_norm_weight, f.eps = q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(eps)
     f.cos, f.sin, f.rope_stride_b = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
     f.cache_pos = cache_pos.data_ptr()
+    if len(_FUSED) >= 512:
+        _FUSED.clear()
+    _FUSED[key] = (bytes(f), tuple(out.shape))
+    return f, out
+
+
+def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
+                      seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace,
+                      probs=None) -> torch.Tensor:
+    """gqa_decode_fused's call through the C ABI; with probs (float32 [B, NH, capacity]), then the step's softmax
+    probabilities into it (bz_gqa_decode_fused_probs: the reference's dbg output of attn_decode_fused)."""
+    f, out = _fused_args(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
+                         seq_lens, kv_start, mask, num_splits, max_seq_len, combine)
+    a = f.base
+    dev = qkv.device
     if probs is not None:
         _check_probs(probs, a, dev)
     lib = kernels.load()
@@ -505,7 +547,7 @@ def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
         ws = workspace if workspace is not None else _stream_workspace(
             dev.index, stream, a.batch * max(1, a.tokens_per_row), a.num_q_heads, a.num_kv_heads, a.head_dim,
             a.capacity, a.num_splits, a.max_seq_len)
-        f.base.workspace, f.base.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()  # a shares f's memory
         sp = ctypes.c_void_p(stream)
         kernels.check(lib.bz_gqa_decode_fused(ctypes.byref(f), sp), "bz_gqa_decode_fused")
         if probs is not None:
