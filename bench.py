@@ -646,8 +646,8 @@ def host_overhead(pkg, dev):
     """Eager host cost per call of the Python entry points on config 1's inputs (B2, 256 positions: every kernel
     takes a few microseconds of GPU time, so the host is the bound): HOST_CALLS back-to-back calls without a
     synchronisation, wall time / calls, median of 5 samples after 50 warmups. 'direct' is the package function (the
-    eager path: argument checks, ctypes structure, C ABI); 'torch_op' the registered operator torch.ops.bz.* called
-    eagerly (what a compiled graph calls, plus the dispatcher)."""
+    eager path: the native binding's checks and the C ABI call; the GEMVs through ctypes); 'torch_op' the registered
+    operator torch.ops.bz.* called eagerly (what a compiled graph calls, plus the dispatcher)."""
     import torch
     from breeze_tts_2_flash_amd import gemv_resid, gqa_decode, gqa_decode_fused, workloads
 

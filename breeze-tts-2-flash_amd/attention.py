@@ -97,6 +97,7 @@ def _stream_workspace(idx: int, stream: int, batch: int, num_q_heads: int, num_k
     key = (idx, stream, batch * num_kv_heads)
     ws = _WS.get(key)
     if ws is not None and ws.numel() >= n:
+        kernels.eager().register_workspace(idx, stream, batch * num_kv_heads, ws)
         return ws
     if torch.cuda.is_current_stream_capturing():
         raise RuntimeError(
@@ -112,6 +113,7 @@ def _stream_workspace(idx: int, stream: int, batch: int, num_q_heads: int, num_k
             if ws is not None:
                 _WS_RETIRED.append(ws)
             _WS[key] = ws = new
+        kernels.eager().register_workspace(idx, stream, batch * num_kv_heads, ws)  # the native path's lookup
         return ws
 
 
@@ -299,7 +301,12 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, se
 
 def _gqa_decode(q, k_cache, v_cache, seq_lens, scale, out, kv_start, mask, num_splits, max_seq_len, combine,
                 workspace) -> torch.Tensor:
-    """gqa_decode's call through the C ABI (the body of the eager path and of torch.ops.bz.gqa_decode)."""
+    """gqa_decode's call through the C ABI (the body of the eager path and of torch.ops.bz.gqa_decode): the native
+    binding when the stream's workspace exists (or none is needed), else here, which makes it."""
+    r = kernels.eager().decode(q, k_cache, v_cache, seq_lens, kv_start, mask, out, scale, num_splits, max_seq_len,
+                               combine, workspace, False)
+    if r is not None:
+        return r
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
     a.seq_lens = _int32_rows(seq_lens, a.batch, "seq_lens", dev).data_ptr()
@@ -354,7 +361,11 @@ def gqa_decode_masked(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
 
 def _gqa_decode_masked(q, k_cache, v_cache, mask, scale, out, num_splits, max_seq_len, combine,
                        workspace) -> torch.Tensor:
-    """gqa_decode_masked's call through the C ABI."""
+    """gqa_decode_masked's call through the C ABI (the native binding first, as in _gqa_decode)."""
+    r = kernels.eager().decode(q, k_cache, v_cache, None, None, mask, out, scale, num_splits, max_seq_len, combine,
+                               workspace, True)
+    if r is not None:
+        return r
     a, out = _fill_args(q, k_cache, v_cache, scale, out, num_splits, max_seq_len, combine)
     dev = q.device
     _check(mask.device == dev, "mask must be on the query's device")
@@ -532,7 +543,13 @@ def _gqa_decode_fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
                       seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace,
                       probs=None) -> torch.Tensor:
     """gqa_decode_fused's call through the C ABI; with probs (float32 [B, NH, capacity]), then the step's softmax
-    probabilities into it (bz_gqa_decode_fused_probs: the reference's dbg output of attn_decode_fused)."""
+    probabilities into it (bz_gqa_decode_fused_probs: the reference's dbg output of attn_decode_fused). Without probs
+    the native binding runs the call when the stream's workspace exists (or one is passed)."""
+    if probs is None:
+        r = kernels.eager().fused(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos,
+                                  scale, out, seq_lens, kv_start, mask, num_splits, max_seq_len, combine, workspace)
+        if r is not None:
+            return r
     f, out = _fused_args(qkv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache, v_cache, cache_pos, scale, out,
                          seq_lens, kv_start, mask, num_splits, max_seq_len, combine)
     a = f.base

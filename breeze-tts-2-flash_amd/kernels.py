@@ -137,16 +137,55 @@ def link_command(objdir: Path, out: Path) -> list[str]:
 STAMP_SOURCE = "bench_stamp.hip"
 STAMP_PATH = PKG_DIR / "libbz_bench_stamp.so"  # bench.py's GPU timestamp kernel; not part of the C ABI
 
+# The native eager binding (csrc/eager_ext.cpp): a CPython extension module built with g++ against torch's headers,
+# host code only, which calls the C ABI functions of the loaded library (eager()).
+EAGER_SOURCE = "eager_ext.cpp"
+EAGER_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM"]
+
+
+def eager_path() -> Path:
+    import sysconfig
+
+    return PKG_DIR / ("_bz_eager" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def eager_id() -> str:
+    """Hash of what the eager module is built from: its source, the C ABI headers and its flags."""
+    h = hashlib.sha256()
+    for f in [CSRC / EAGER_SOURCE] + sorted(INCLUDE.glob("*.h")):
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    h.update(" ".join(EAGER_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
+def eager_command(out: Path) -> list[str]:
+    """g++ command for the eager module: torch's headers and libraries, the HIP runtime's headers and library."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    torch_lib = cpp_extension.library_paths()[0]
+    incs = [f"-I{d}" for d in cpp_extension.include_paths()] + [f"-I{sysconfig.get_paths()['include']}",
+                                                                  f"-I{rocm}/include", f"-I{INCLUDE}"]
+    return ["g++", *EAGER_FLAGS, f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+            f"-DBZ_EAGER_BUILD_ID=\"{eager_id()}\"", *incs, str(CSRC / EAGER_SOURCE), "-o", str(out),
+            f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", f"-L{rocm}/lib",
+            "-lamdhip64", f"-Wl,-rpath,{torch_lib}", f"-Wl,-rpath,{rocm}/lib"]
+
 
 def build(verbose: bool = False) -> Path:
-    """Compile libbz_gqa_decode.so for gfx950 in-tree (always recompiles), and bench.py's timestamp helper
-    libbz_bench_stamp.so. Returns the path of libbz_gqa_decode.so."""
+    """Compile libbz_gqa_decode.so for gfx950 in-tree (always recompiles), bench.py's timestamp helper
+    libbz_bench_stamp.so and the native eager binding (_bz_eager). Returns the path of libbz_gqa_decode.so."""
     tmp = LIB_PATH.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="bz_gqa_build_") as d:
         objdir = Path(d)
         cmds = compile_commands(objdir)
         stamp_tmp = STAMP_PATH.with_suffix(".so.tmp")
         cmds.append([hipcc(), *HIPCC_FLAGS, "-shared", str(CSRC / STAMP_SOURCE), "-o", str(stamp_tmp)])
+        eager_tmp = objdir / eager_path().name
+        cmds.append(eager_command(eager_tmp))
 
         def run(cmd):
             if verbose:
@@ -159,6 +198,8 @@ def build(verbose: bool = False) -> Path:
             if res.returncode != 0:
                 raise RuntimeError(f"hipcc failed ({res.returncode}) on {cmd[-3]}:\n{res.stderr[-4000:]}")
         os.replace(stamp_tmp, STAMP_PATH)
+        shutil.copyfile(eager_tmp, eager_path().with_suffix(".tmp"))
+        os.replace(eager_path().with_suffix(".tmp"), eager_path())
         res = run(link_command(objdir, tmp))
         if res.returncode != 0:
             raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{res.stderr[-4000:]}")
@@ -225,6 +266,42 @@ def load() -> ctypes.CDLL:
                                "g.build()')")
         _LIB = lib
         return lib
+
+
+_EAGER = None
+
+
+def eager():
+    """The native eager binding, imported once per process and bound to the loaded library's C ABI functions.
+    Raises if it is missing or was built from other sources (no fallback)."""
+    global _EAGER
+    if _EAGER is not None:
+        return _EAGER
+    with _LOCK:
+        if _EAGER is not None:
+            return _EAGER
+    lib = load()
+    import importlib.util
+
+    import torch  # noqa: F401  (the module links against torch's libraries)
+
+    path = eager_path()
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    spec = importlib.util.spec_from_file_location("_bz_eager", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    built, current = mod.build_id(), eager_id()
+    if built != current:
+        raise RuntimeError(f"{path} was built from other sources or flags (build id {built}, the sources next to it "
+                           f"hash to {current}): rebuild it (python -c 'import __graft_entry__ as g; g.build()')")
+    addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
+    mod.bind(addr(lib.bz_gqa_decode), addr(lib.bz_gqa_decode_masked), addr(lib.bz_gqa_decode_noalloc),
+             addr(lib.bz_gqa_decode_fused), addr(lib.bz_status_string), addr(lib.bz_gqa_decode_workspace_size))
+    with _LOCK:
+        if _EAGER is None:
+            _EAGER = mod
+    return _EAGER
 
 
 _TC = None  # torch._C, bound on first use (this module does not import torch at load time)
