@@ -130,8 +130,6 @@ class GpuStamps:
     _lib = None
 
     def __init__(self, dev, n=2):
-        import ctypes
-
         import torch
 
         GpuStamps.library()
@@ -144,8 +142,6 @@ class GpuStamps:
 
     @staticmethod
     def library():
-        import ctypes
-
         from breeze_tts_2_flash_amd import kernels
 
         if GpuStamps._lib is None:
@@ -158,8 +154,6 @@ class GpuStamps:
         return GpuStamps._lib
 
     def stamp(self, i):
-        import ctypes
-
         import torch
 
         stream = torch.cuda.current_stream(self.dev).cuda_stream
@@ -349,8 +343,6 @@ def time_stream_floor(dev, sizes):
     are (EXTRA_CALLS launches in one HIP graph between GPU stamps, 2 untimed lead launches, rotating over ROTATE_BYTES,
     after a flush), on 256, 512 and 1024 workgroups. sizes: {name: bytes per launch}. Returns
     {name: ({workgroups: µs per launch}, bytes read per launch)}."""
-    import ctypes
-
     import torch
 
     lib = GpuStamps.library()
