@@ -198,9 +198,13 @@ const at::Tensor* stream_workspace(int idx, hipStream_t stream, const bz_gqa_dec
   return &it->second;
 }
 
+// Whether the stream is being captured into a graph; a failing query raises, as torch's
+// is_current_stream_capturing does (the Python path's check).
 bool capturing(hipStream_t s) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  return hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusActive;
+  const hipError_t e = hipStreamIsCapturing(s, &st);
+  if (e != hipSuccess) throw Error{std::string("hipStreamIsCapturing: ") + hipGetErrorString(e)};
+  return st == hipStreamCaptureStatusActive;
 }
 
 PyObject* result(PyObject* out_obj, const at::Tensor& out) {
