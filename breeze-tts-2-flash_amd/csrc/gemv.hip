@@ -16,6 +16,9 @@
 //     accumulators are summed over the wave with DPP inside 16-lane rows and transposed permlane swaps across rows,
 //     so each lane of a row ends with one finished output, written with the epilogue by that row's first lane.
 // The weight loads carry the non-temporal hint: 2.8 GB of weights stream through per decode step.
+// Where it measured faster (4096 < k <= 6144 at any M, the backbone's down projection; 1024 < k <= 2048 at M >= 3)
+// a block-ordered kernel runs instead: a workgroup streams its rows as one contiguous block, every thread holding one
+// x vector for all of its rows, and the sums are reduced over the workgroup once, at the end (gemv_block_kernel).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -377,6 +380,157 @@ __global__ void __launch_bounds__(gemv_threads<KC>())
   }
 }
 
+// Block-ordered GEMV: a workgroup of NT threads owns R = Q * NA output rows (2 R weight rows for the SiLU * up
+// epilogue: the gate rows, then the up rows) and streams them as one contiguous block. A row holds KV = NT / Q vectors
+// of 16 bytes (k <= 8 KV; the vectors past k read 0); load i of thread t reads vector t % KV of row Q i + t / KV, so
+// each wave stays inside one row, every thread needs the same x vector (t % KV) for all of its rows, and all NS loads
+// per thread go out at once. Against the wave-per-row kernel above this keeps the workgroup's bytes in flight
+// contiguous (the wave-per-row kernel with x in LDS holds a third of each of eight rows 12 KB apart at k = 6144) and
+// each workgroup reads x once (with x in registers there every wave reads its own: 32 MB of L2 traffic for q | k | v at
+// M = 4). The sums of a row slot are reduced over the waves of its row group once, at the end: DPP and transposed
+// swaps inside each wave, then the group's waves through LDS in wave order.
+template <int M, int NT, int Q, int NA, bool NORM, int EPI>
+__global__ void __launch_bounds__(NT)
+    gemv_block_kernel(const uint16_t* w0, const uint16_t* w1, const uint16_t* w2, int n0, int n1, int ntot, int k,
+                      const uint16_t* x, int64_t ldx, const GemvParams args) {
+  GemvParams p = args;
+  p.w0 = w0;
+  p.w1 = w1;
+  p.w2 = w2;
+  p.n0 = n0;
+  p.n1 = n1;
+  p.ntot = ntot;
+  p.k = k;
+  p.x = x;
+  p.ldx = ldx;
+  constexpr int NW = NT / kWave, KV = NT / Q, WPG = NW / Q;  // waves per row group
+  static_assert(KV % kWave == 0, "a wave reads within one row");
+  constexpr bool SILU = EPI == BZ_GEMV_SILU_MUL;
+  constexpr int NS = SILU ? 2 * NA : NA;  // weight-row slots per thread (SiLU: the gate slots, then the up slots)
+  constexpr int R = Q * NA;               // output rows per workgroup
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int g = wave_uniform(wave / WPG);  // row group: the weight resources below stay scalar
+  const int kv = tid % KV;
+  const int row0 = blockIdx.x * R;
+
+  // x (and the norm weight) first, then every weight load; the prologue waits for x alone
+  const Rsrc rx = span_rsrc(p.x, (int)(((int64_t)(M - 1) * p.ldx + p.k) * 2));
+  uint4 xv[M], nwv = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const uint32_t off = 8 * kv < p.k ? (uint32_t)(m * p.ldx + 8 * kv) * 2 : 0xfffffff0u;  // past k: reads 0
+    xv[m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+  }
+  if (NORM)
+    nwv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(span_rsrc(p.nw, p.k * 2), 16 * kv, 0, 0));
+  uint4 wt[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool up = SILU && s >= NA;
+    const int n = row0 + Q * (up ? s - NA : s) + g;
+    const int bytes = n < p.ntot ? p.k * 2 : 0;  // a row past the last output: an empty resource, its loads read 0
+    const uint16_t* base;
+    if (SILU) {
+      base = (up ? p.w1 : p.w0) + (int64_t)n * p.k;
+    } else {
+      base = n < p.n0 ? p.w0 + (int64_t)n * p.k
+           : n < p.n0 + p.n1 ? p.w1 + (int64_t)(n - p.n0) * p.k
+                             : p.w2 + (int64_t)(n - p.n0 - p.n1) * p.k;
+    }
+    wt[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(span_rsrc(base, bytes), 16 * kv, 0, kStream));
+  }
+  // the residual value of the output this thread writes (thread f < R * M: row f / M, batch row f % M); loads past
+  // the residual matrix read 0 without a memory access, and values past the output rows are never used
+  float resv = 0.f;
+  if (EPI == BZ_GEMV_RESIDUAL) {
+    const Rsrc rr = span_rsrc(p.res, (int)(((int64_t)(M - 1) * p.ldr + p.ntot) * 2));
+    const int f = tid % (R * M), n = row0 + f / M, m = f % M;
+    resv = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rr, (uint32_t)(((int64_t)m * p.ldr + n) * 2), 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (NORM) {
+    // every row group holds all of x: the sum of squares over the waves of group 0
+    __shared__ float s_ss[NW][M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float f[8], ss = 0.f;
+      unpack8(xv[m], f);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) ss = fmaf(f[t], f[t], ss);
+      ss = wave_sum(ss);
+      if (lane == 0) s_ss[wave][m] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) tot += s_ss[w][m];
+      const float rs = rsqrtf(tot * (1.f / (float)p.k) + p.eps);
+      float f[8], w[8];
+      unpack8(xv[m], f);
+      unpack8(nwv, w);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) f[t] *= rs;
+      round8(f);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) f[t] *= w[t];
+      xv[m] = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                         pack_bf16x2(f[6], f[7]));
+    }
+  }
+
+  // flat value s * M + m, summed over the wave: row q of the wave's sums holds flat value 4 c + q
+  constexpr int NV = NS * M, NQ = (NV + 3) / 4;
+  float flat[4 * NQ];
+#pragma unroll
+  for (int v = 0; v < 4 * NQ; ++v) flat[v] = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4& w = wt[s];
+      float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), __builtin_bit_cast(bf16x2_t, xv[m].x),
+                                                0.f, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), __builtin_bit_cast(bf16x2_t, xv[m].y), a,
+                                          false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), __builtin_bit_cast(bf16x2_t, xv[m].z), a,
+                                          false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, xv[m].w), a,
+                                          false);
+      flat[s * M + m] = row_sum<16>(a);
+    }
+  __shared__ float s_red[NW][4 * NQ];
+#pragma unroll
+  for (int c = 0; c < NQ; ++c) {
+    const float v = rows_sum4(flat[4 * c], flat[4 * c + 1], flat[4 * c + 2], flat[4 * c + 3]);
+    if (lane % 16 == 0) s_red[wave][4 * c + lane / 16] = v;
+  }
+  __syncthreads();
+  // thread f < R * M writes row row0 + f / M of batch row f % M: slot a = (f / M) / Q of row group (f / M) % Q
+  if (tid >= R * M) return;
+  const int rr = tid / M, m = tid % M, n = row0 + rr, a = rr / Q, gg = rr % Q;
+  if (n >= p.ntot) return;
+  float red = 0.f, upv = 0.f;
+#pragma unroll
+  for (int w = 0; w < WPG; ++w) {
+    red += s_red[gg * WPG + w][a * M + m];
+    if (SILU) upv += s_red[gg * WPG + w][(NA + a) * M + m];
+  }
+  float v;
+  if (EPI == BZ_GEMV_PLAIN) {
+    v = red;
+  } else if (EPI == BZ_GEMV_RESIDUAL) {
+    v = resv + bf16_to_f32(f32_to_bf16(red));
+  } else {
+    const float gt = bf16_to_f32(f32_to_bf16(red));
+    const float u = bf16_to_f32(f32_to_bf16(upv));
+    v = bf16_to_f32(f32_to_bf16(gt / (1.f + expf(-gt)))) * u;
+  }
+  p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(v);
+}
+
 // Standalone row RMSNorm, one workgroup per row (bb_fused.cu:219-248).
 __global__ void __launch_bounds__(kGemvThreads) rmsnorm_kernel(const uint16_t* x, int64_t ldx, const uint16_t* w,
                                                                float eps, uint16_t* y, int64_t ldy, int k) {
@@ -467,6 +621,64 @@ GemvFn pick_gemv(int m, int kc, int r, int epi, bool norm, bool pace) {
   }
 }
 
+// The block-ordered kernel where it measured faster than the wave-per-row kernel (cold, graph replay, M = 1 / 2 / 4):
+//   4096 < k <= 6144, any M: 768 threads, one row per load instruction (down at k = 6144: 6.71 / 6.77 / 7.83 us ->
+//     5.89 / 6.19 / 6.76);
+//   1024 < k <= 2048 and M >= 3: 512 threads, two rows per load instruction (q | k | v at M = 4: 6.99 -> 5.80 us;
+//     o_proj and gate / up within 0.1 us). At M <= 2 there the wave-per-row kernel with x in registers stays faster
+//     (q | k | v 4.98 against 5.12 us, o_proj 3.33 against 3.49).
+// Eight row slots per thread (256 workgroups at the backbone's down and q | k | v), four where eight leave fewer than
+// 256 workgroups (o_proj), and four gate plus four up slots for the SiLU * up epilogue (eight of each: gate / up 11.7
+// against 10.4 us at M = 2).
+constexpr int kBlockMinGrid = 256;
+
+template <int M, int NT, int Q, int NA>
+GemvFn pick_block_epi(int epi, bool norm) {
+  if (epi == BZ_GEMV_PLAIN)
+    return norm ? gemv_block_kernel<M, NT, Q, NA, true, BZ_GEMV_PLAIN>
+                : gemv_block_kernel<M, NT, Q, NA, false, BZ_GEMV_PLAIN>;
+  if (epi == BZ_GEMV_RESIDUAL) return norm ? nullptr : gemv_block_kernel<M, NT, Q, NA, false, BZ_GEMV_RESIDUAL>;
+  return nullptr;
+}
+template <int M, int NT, int Q>
+GemvFn pick_block_na(int na, int epi, bool norm) {
+  if (epi == BZ_GEMV_SILU_MUL)
+    return norm ? gemv_block_kernel<M, NT, Q, 4, true, BZ_GEMV_SILU_MUL>
+                : gemv_block_kernel<M, NT, Q, 4, false, BZ_GEMV_SILU_MUL>;
+  if constexpr (Q == 1) {
+    (void)na;
+    return pick_block_epi<M, NT, Q, 8>(epi, norm);  // one row per instruction: eight slots
+  } else {
+    return na == 8 ? pick_block_epi<M, NT, Q, 8>(epi, norm) : pick_block_epi<M, NT, Q, 4>(epi, norm);
+  }
+}
+// The block kernel for this call, its workgroup size and grid; nullptr where the wave-per-row kernel is taken.
+GemvFn pick_block(int m, int k, int ntot, int epi, bool norm, int* threads, int* grid) {
+  int q;
+  if (k > 4096 && k <= 6144) {
+    q = 1;
+    *threads = 768;
+  } else if (k > 1024 && k <= 2048 && m >= 3) {
+    q = 2;
+    *threads = 512;
+  } else {
+    return nullptr;
+  }
+  int na = 8;
+  if (epi == BZ_GEMV_SILU_MUL || (q == 2 && (ntot + 8 * q - 1) / (8 * q) < kBlockMinGrid)) na = 4;
+  *grid = (ntot + q * na - 1) / (q * na);
+  if (q == 1) {
+    switch (m) {
+      case 1: return pick_block_na<1, 768, 1>(na, epi, norm);
+      case 2: return pick_block_na<2, 768, 1>(na, epi, norm);
+      case 3: return pick_block_na<3, 768, 1>(na, epi, norm);
+      case 4: return pick_block_na<4, 768, 1>(na, epi, norm);
+      default: return nullptr;
+    }
+  }
+  return m == 3 ? pick_block_na<3, 512, 2>(na, epi, norm) : pick_block_na<4, 512, 2>(na, epi, norm);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Output rows per wave. With x in registers every wave loads its own x, so two rows per wave halve that L2 traffic
@@ -517,20 +729,6 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   if (a->epilogue == BZ_GEMV_RESIDUAL && ((int64_t)(a->m - 1) * a->res_stride + ntot) * 2 > INT32_MAX)
     return BZ_ERR_SHAPE;  // the residual: 32-bit byte offsets
 
-  const int kc = kc_for(a->m, a->k);
-  const int r = rows_per_wave(ntot, a->epilogue, kc);
-  const int threads = kc > 0 ? kGemvThreads : kGemvLdsThreads;
-  const int rows_per_block = threads / kWave * r;
-  const int grid = (ntot + rows_per_block - 1) / rows_per_block;
-  bool pace = kc > 0 && grid >= kPaceMinGrid;
-  if (pace && (a->epilogue == BZ_GEMV_SILU_MUL ? 2 * r : r) * kc < kPaceMinLoads) {
-    int cus = 0;
-    const int rc = bz::device_cu_count(&cus);
-    if (rc != BZ_OK) return rc;
-    pace = grid > cus;
-  }
-  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr, pace);
-  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   GemvParams p;
   p.x = static_cast<const uint16_t*>(a->x);
   p.ldx = a->x_stride;
@@ -548,6 +746,26 @@ __attribute__((visibility("default"))) int bz_gemv(const bz_gemv_args* a, hipStr
   p.ldy = a->y_stride;
   p.res = static_cast<const uint16_t*>(a->res);
   p.ldr = a->res_stride;
+  int bthreads = 0, bgrid = 0;
+  if (GemvFn bf = pick_block(a->m, a->k, ntot, a->epilogue, a->norm_weight != nullptr, &bthreads, &bgrid)) {
+    hipLaunchKernelGGL(bf, dim3(bgrid), dim3(bthreads), 0, stream, p.w0, p.w1, p.w2, p.n0, p.n1, p.ntot, p.k, p.x,
+                       p.ldx, p);
+    return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+  }
+  const int kc = kc_for(a->m, a->k);
+  const int r = rows_per_wave(ntot, a->epilogue, kc);
+  const int threads = kc > 0 ? kGemvThreads : kGemvLdsThreads;
+  const int rows_per_block = threads / kWave * r;
+  const int grid = (ntot + rows_per_block - 1) / rows_per_block;
+  bool pace = kc > 0 && grid >= kPaceMinGrid;
+  if (pace && (a->epilogue == BZ_GEMV_SILU_MUL ? 2 * r : r) * kc < kPaceMinLoads) {
+    int cus = 0;
+    const int rc = bz::device_cu_count(&cus);
+    if (rc != BZ_OK) return rc;
+    pace = grid > cus;
+  }
+  GemvFn fn = pick_gemv(a->m, kc, r, a->epilogue, a->norm_weight != nullptr, pace);
+  if (fn == nullptr) return BZ_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), kc > 0 ? 0 : lds, stream, p.w0, p.w1, p.w2, p.n0, p.n1, p.ntot,
                      p.k, p.x, p.ldx, p);
   return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;

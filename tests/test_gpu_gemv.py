@@ -1,7 +1,8 @@
 """GPU parity of the backbone decode GEMVs (bz_gemv / bz_rmsnorm through gemv_seg, gemv_resid, gemv_gateup and
 rmsnorm) against oracle.gemv at the reference backbone's shapes (hidden 2048, q / k / v 2048 / 1024 / 1024,
 intermediate 6144, the CFG pair M = 2) and at edge shapes (M = 1..4, K not a multiple of the tile, output rows not a
-multiple of the workgroup's, strided x, missing segments).
+multiple of the workgroup's, strided x, missing segments), on both kernels: the wave-per-row kernel and the
+block-ordered one (4096 < K <= 6144 at any M, 1024 < K <= 2048 at M >= 3).
 
 Tolerance: the outputs are bf16 roundings of fp32 sums whose order differs from the float64 oracle's, so a value on a
 rounding boundary can move by one bf16 ulp (two through the SiLU chain): |got - ref| <= 2^-6 |ref| + 2^-6 rms(ref row),
@@ -94,7 +95,11 @@ def test_backbone_down_residual(device, bb):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
-@pytest.mark.parametrize("K,N", [(1000, 37), (1032, 129), (3072, 520)])
+# K 1000 and 3072: the wave-per-row kernel (x in registers, x in LDS); K 1032, 1800, 2048 at M >= 3 and K 4104, 6144
+# at any M: the block-ordered kernel, with rows past k's last full vector block (1032, 1800, 4104) and output rows
+# that are not a multiple of a workgroup's (37, 129, 130, 300, 520)
+@pytest.mark.parametrize("K,N", [(1000, 37), (1032, 129), (3072, 520), (1800, 130), (2048, 300), (4104, 37),
+                                 (6144, 520)])
 @pytest.mark.parametrize("kind", ["plain", "norm", "residual", "silu"])
 def test_edge_shapes(device, M, K, N, kind):
     rng = np.random.default_rng(M * 1000 + K + N)
@@ -137,6 +142,21 @@ def test_segments_split_anywhere(device):
     gemv_seg(dev_bf16(x, device), None, 0.0, dev_bf16(W[0], device), torch.empty(0), dev_bf16(W[2], device), y2)
     torch.cuda.synchronize()
     assert_gemv_close(host_bits(y2), gemv_ref(x, [W[0], W[2]]), "segments without W1")
+
+
+@pytest.mark.parametrize("M,K", [(2, 6144), (4, 6144), (3, 2048), (4, 2048)])
+def test_block_kernel_segments_and_strides(device, M, K):
+    # the block-ordered kernel's row groups and slots across q | k | v segment boundaries (inside a workgroup's rows
+    # and inside a row group), a strided x and y, and the norm prologue
+    rng = np.random.default_rng(M * 7 + K)
+    xs = rand_bits(rng, M, K + 40, scale=2.0)
+    W = [rand_bits(rng, n, K, scale=K ** -0.5) for n in (21, 6, 35)]
+    nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    ys = torch.empty(M, 70, dtype=torch.bfloat16, device=device)
+    y = ys[:, :62]
+    gemv_seg(dev_bf16(xs, device)[:, :K], dev_bf16(nw, device), 1e-6, *(dev_bf16(w, device) for w in W), y)
+    torch.cuda.synchronize()
+    assert_gemv_close(host_bits(y), gemv_ref(xs[:, :K], W, nw, 1e-6), f"segments M={M} K={K}")
 
 
 def test_identity_weights_exact(device):
