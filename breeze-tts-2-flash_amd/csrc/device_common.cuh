@@ -115,6 +115,82 @@ __device__ __forceinline__ float rows_sum4(float v0, float v1, float v2, float v
   return s + t;       // [v0 v1 v2 v3], each summed over the four rows
 }
 
+// Sum over the 64 lanes of a wave of NV values v[0..NV) (NV a power of two up to 64), transposed: each level pairs
+// the lanes across one lane bit (bit 5 and bit 4 by the permlane swaps; bits 3, 2, 1, 0 by DPP row_ror:8,
+// row_half_mirror, quad_perm [2,3,0,1] and [1,0,3,2]), and while more than one value is left every lane keeps half of
+// them (the upper half where its bit is set) and adds its partner's share of that half, so the values halve at every
+// level (NV - 1 swaps or DPP moves in all, against four DPP adds per value for row sums). The lanes each pairing
+// joins are always disjoint (the pairings differ on each level), so after the six levels lane L holds, in its v[0],
+// the total of value transposed_index<NV>(L), bit for bit the same in every lane that holds that value.
+template <int H, int CTRL>
+__device__ __forceinline__ void dpp_level(float* v, bool hi) {
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float keep = hi ? v[i + H] : v[i], send = hi ? v[i] : v[i + H];
+    v[i] = keep + dpp<CTRL>(send);
+  }
+}
+template <int H>
+__device__ __forceinline__ void swap_level(float* v, bool upper32) {
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    if (upper32) swap32(v[i], v[i + H]);
+    else swap16(v[i], v[i + H]);
+    v[i] += v[i + H];
+  }
+}
+template <int NV>
+__device__ __forceinline__ float transposed_sum(float (&v)[NV], int lane) {
+  static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "a power of two up to 64 values");
+  // values left before the levels on bits 5, 4, 3, 2, 1, 0
+  constexpr int N5 = NV, N4 = N5 > 1 ? N5 / 2 : 1, N3 = N4 > 1 ? N4 / 2 : 1, N2 = N3 > 1 ? N3 / 2 : 1,
+                N1 = N2 > 1 ? N2 / 2 : 1, N0 = N1 > 1 ? N1 / 2 : 1;
+  float t;
+  if constexpr (N5 > 1) {
+    swap_level<N5 / 2>(v, true);  // bit 5: lanes 0..31 against 32..63
+  } else {
+    t = v[0];
+    swap32(v[0], t);
+    v[0] += t;
+  }
+  if constexpr (N4 > 1) {
+    swap_level<N4 / 2>(v, false);  // bit 4: rows 0 / 2 against rows 1 / 3
+  } else {
+    t = v[0];
+    swap16(v[0], t);
+    v[0] += t;
+  }
+  if constexpr (N3 > 1) dpp_level<N3 / 2, 0x128>(v, lane & 8);  // bit 3: row_ror:8
+  else v[0] += dpp<0x128>(v[0]);
+  if constexpr (N2 > 1) dpp_level<N2 / 2, 0x141>(v, lane & 4);  // bit 2: row_half_mirror (lane i <-> 7 - i)
+  else v[0] += dpp<0x141>(v[0]);
+  if constexpr (N1 > 1) dpp_level<N1 / 2, 0x4e>(v, lane & 2);  // bit 1: quad_perm [2,3,0,1]
+  else v[0] += dpp<0x4e>(v[0]);
+  if constexpr (N0 > 1) dpp_level<N0 / 2, 0xb1>(v, lane & 1);  // bit 0: quad_perm [1,0,3,2]
+  else v[0] += dpp<0xb1>(v[0]);
+  return v[0];
+}
+// The value whose total lane L holds after transposed_sum<NV>: bit 5 of L selects the upper half of the values, bit 4
+// the upper half of that half, and so on for as many levels as halve NV.
+template <int NV>
+__device__ __forceinline__ int transposed_index(int lane) {
+  int idx = 0, h = NV / 2;
+  const int bits[6] = {32, 16, 8, 4, 2, 1};
+#pragma unroll
+  for (int b = 0; b < 6; ++b) {
+    if (h >= 1 && (lane & bits[b])) idx += h;
+    h /= 2;
+  }
+  return idx;
+}
+// Whether lane L is the first of the lanes holding its value (its bits below the transposed levels are zero).
+template <int NV>
+__device__ __forceinline__ bool transposed_writer(int lane) {
+  int levels = 0;
+  for (int n = NV; n > 1; n /= 2) ++levels;
+  return (lane & ((1 << (6 - levels)) - 1)) == 0;
+}
+
 // Max over the four 16-lane rows of a wave of each of the N values x[i]; every lane ends with all N maxima.
 template <int N>
 __device__ __forceinline__ void rows_max(float (&x)[N]) {

@@ -481,11 +481,12 @@ __global__ void __launch_bounds__(NT)
     }
   }
 
-  // flat value s * M + m, summed over the wave: row q of the wave's sums holds flat value 4 c + q
-  constexpr int NV = NS * M, NQ = (NV + 3) / 4;
-  float flat[4 * NQ];
+  // flat value s * M + m (zero-padded to a power of two), summed over the wave by the transposed sum: one total per
+  // value, written to LDS by the first lane that holds it
+  constexpr int NV = NS * M, NP = NV <= 4 ? 4 : NV <= 8 ? 8 : NV <= 16 ? 16 : NV <= 32 ? 32 : 64;
+  float flat[NP];
 #pragma unroll
-  for (int v = 0; v < 4 * NQ; ++v) flat[v] = 0.f;
+  for (int v = 0; v < NP; ++v) flat[v] = 0.f;
 #pragma unroll
   for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -499,14 +500,11 @@ __global__ void __launch_bounds__(NT)
                                           false);
       a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, xv[m].w), a,
                                           false);
-      flat[s * M + m] = row_sum<16>(a);
+      flat[s * M + m] = a;
     }
-  __shared__ float s_red[NW][4 * NQ];
-#pragma unroll
-  for (int c = 0; c < NQ; ++c) {
-    const float v = rows_sum4(flat[4 * c], flat[4 * c + 1], flat[4 * c + 2], flat[4 * c + 3]);
-    if (lane % 16 == 0) s_red[wave][4 * c + lane / 16] = v;
-  }
+  const float tot = transposed_sum<NP>(flat, lane);
+  __shared__ float s_red[NW][NP];
+  if (transposed_writer<NP>(lane)) s_red[wave][transposed_index<NP>(lane)] = tot;
   __syncthreads();
   // thread f < R * M writes row row0 + f / M of batch row f % M: slot a = (f / M) / Q of row group (f / M) % Q
   if (tid >= R * M) return;
