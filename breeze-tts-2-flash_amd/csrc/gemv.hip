@@ -619,12 +619,13 @@ GemvFn pick_gemv(int m, int kc, int r, int epi, bool norm, bool pace) {
   }
 }
 
-// The block-ordered kernel where it measured faster than the wave-per-row kernel (cold, graph replay, M = 1 / 2 / 4):
-//   4096 < k <= 6144, any M: 768 threads, one row per load instruction (down at k = 6144: 6.71 / 6.77 / 7.83 us ->
-//     5.89 / 6.19 / 6.76);
-//   1024 < k <= 2048 and M >= 3: 512 threads, two rows per load instruction (q | k | v at M = 4: 6.99 -> 5.80 us;
-//     o_proj and gate / up within 0.1 us). At M <= 2 there the wave-per-row kernel with x in registers stays faster
-//     (q | k | v 4.98 against 5.12 us, o_proj 3.33 against 3.49).
+// The block-ordered kernel where it measured faster than the wave-per-row kernel (cold, graph replay, us per call,
+// wave-per-row -> block):
+//   4096 < k <= 6144, any M: 768 threads, one row per load instruction (down at k = 6144, M = 1 / 2 / 4: 6.71 / 6.77 /
+//     7.50 -> 5.93 / 6.01 / 6.30);
+//   1024 < k <= 2048 and M >= 3: 512 threads, two rows per load instruction (M = 4: q | k | v 7.04 -> 5.41, gate / up
+//     12.75 -> 12.0, o_proj 3.85 -> 3.58). At M <= 2 the wave-per-row kernel with x in registers stays faster there
+//     (the backbone step at M = 2 on one box: gate / up 9.70 against 9.92 us, the step 852 against 861 us).
 // Eight row slots per thread (256 workgroups at the backbone's down and q | k | v), four where eight leave fewer than
 // 256 workgroups (o_proj), and four gate plus four up slots for the SiLU * up epilogue (eight of each: gate / up 11.7
 // against 10.4 us at M = 2).

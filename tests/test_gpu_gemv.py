@@ -95,9 +95,9 @@ def test_backbone_down_residual(device, bb):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
-# K 1000 and 3072: the wave-per-row kernel (x in registers, x in LDS); K 1032, 1800, 2048 at M >= 3 and K 4104, 6144
-# at any M: the block-ordered kernel, with rows past k's last full vector block (1032, 1800, 4104) and output rows
-# that are not a multiple of a workgroup's (37, 129, 130, 300, 520)
+# K 1000 and 3072: the wave-per-row kernel (x in registers, x in LDS); K 1032, 1800 and 2048 at M >= 3 and K 4104
+# and 6144 at any M: the block-ordered kernel, with rows past k's last full vector block (1032, 1800, 4104) and output
+# rows that are not a multiple of a workgroup's (37, 129, 130, 300, 520)
 @pytest.mark.parametrize("K,N", [(1000, 37), (1032, 129), (3072, 520), (1800, 130), (2048, 300), (4104, 37),
                                  (6144, 520)])
 @pytest.mark.parametrize("kind", ["plain", "norm", "residual", "silu"])
@@ -144,7 +144,7 @@ def test_segments_split_anywhere(device):
     assert_gemv_close(host_bits(y2), gemv_ref(x, [W[0], W[2]]), "segments without W1")
 
 
-@pytest.mark.parametrize("M,K", [(2, 6144), (4, 6144), (3, 2048), (4, 2048)])
+@pytest.mark.parametrize("M,K", [(2, 6144), (4, 6144), (1, 2048), (3, 2048), (4, 2048)])
 def test_block_kernel_segments_and_strides(device, M, K):
     # the block-ordered kernel's row groups and slots across q | k | v segment boundaries (inside a workgroup's rows
     # and inside a row group), a strided x and y, and the norm prologue

@@ -7,9 +7,9 @@ import pytest
 import torch
 
 import breeze_tts_2_flash_amd as bz
-from oracle.attention import interval_mask, rope_cos_sin
+from oracle.attention import interval_mask, qk_norm_rope, rope_cos_sin
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
-from oracle.gemv import decoder_layer
+from oracle.gemv import decoder_layer, gemv
 
 pytestmark = pytest.mark.gpu
 
@@ -54,7 +54,7 @@ def test_decoder_layer_matches_oracle(device, x_scale):
     p, kc, vc, x = make_layer(31, x_scale)
     pos, pad = 999, [0, 64]
     cos, sin = (f32_to_bf16(t) for t in rope_cos_sin([pos, pos], D))
-    ref, k2, v2 = decoder_layer(x, p, cos, sin, kc, vc, pos, np.array([pos + 1, pos + 1]), kv_start=np.array(pad))
+    ref, _, _ = decoder_layer(x, p, cos, sin, kc, vc, pos, np.array([pos + 1, pos + 1]), kv_start=np.array(pad))
 
     pd = {k: (dev(v, device) if isinstance(v, np.ndarray) else v) for k, v in p.items()}
     kcd, vcd = dev(kc, device), dev(vc, device)
@@ -74,10 +74,19 @@ def test_decoder_layer_matches_oracle(device, x_scale):
           f"exact {(bits(out) == ref).mean():.4f}", flush=True)
     # the attention output carries |d| <= 2e-3 + 1e-2 |ref| into o_proj; the GEMVs add bf16 rounding differences
     assert (err <= 2.0 ** -5 * np.abs(want) + 1e-2 * rms).all()
-    # the new k (normed, roped) and v were written at slot pos, bit for bit except for last-place rounding of k
+    # q | k | v within the GEMV's rounding of the oracle's; the new v (raw) and k (normed, roped) written at slot pos are
+    # the oracle prologue's of the device's own q | k | v, v bit for bit and k up to its last-place rounding (a k
+    # value one bf16 ulp off the oracle's GEMV can move a roped k, a difference of two products, by more than that)
+    qkv = bits(bufs[0])
+    g_qkv, w_qkv = bf16_to_f32(qkv).astype(np.float64), bf16_to_f32(gemv(x, [p["wq"], p["wk"], p["wv"]], p["ln1"],
+                                                                          p["eps"])).astype(np.float64)
+    q_rms = np.sqrt((w_qkv ** 2).mean(axis=-1, keepdims=True))
+    assert (np.abs(g_qkv - w_qkv) <= 2.0 ** -6 * np.abs(w_qkv) + 2.0 ** -6 * q_rms).all()
+    k_raw = qkv[:, NQ:NQ + NK].reshape(2, NK // D, D)
+    k_want = qk_norm_rope(k_raw, p["kn"], p["qk_eps"], cos[:, None], sin[:, None])
     kd = bits(kcd)[:, :, pos]
-    assert np.array_equal(bits(vcd)[:, :, pos], v2[:, :, pos])
-    assert (np.abs(bf16_to_f32(kd) - bf16_to_f32(k2[:, :, pos])) <= np.abs(bf16_to_f32(k2[:, :, pos])) * 2 ** -7 + 1e-30).all()
+    assert np.array_equal(bits(vcd)[:, :, pos], qkv[:, NQ + NK:].reshape(2, NK // D, D))
+    assert (np.abs(bf16_to_f32(kd) - bf16_to_f32(k_want)) <= np.abs(bf16_to_f32(k_want)) * 2 ** -7 + 1e-30).all()
 
 
 def test_two_layers_in_a_hip_graph(device):
