@@ -1,10 +1,11 @@
 // Native eager binding of the decode-attention entry points (the package's gqa_decode, gqa_decode_masked and
-// gqa_decode_fused without probs): the argument checks, the output allocation, the device switch, the stream and
-// workspace lookup and the C ABI call in one call from Python, as the reference binds its ops with pybind
-// (flash/csrc/bb_attn.cu:462-469). The Python functions call it first; it returns None when the call needs a
+// gqa_decode_fused without probs) and of the backbone GEMVs (gemv_seg, gemv_resid, gemv_gateup, rmsnorm): the
+// argument checks, the output allocation, the device switch, the stream and workspace lookup and the C ABI call in
+// one call from Python, as the reference binds its ops with pybind (flash/csrc/bb_attn.cu:462-469,
+// flash/csrc/bb_fused.cu:370-377). The attention functions call it first; it returns None when the call needs a
 // workspace that does not exist yet, and the Python path then allocates it (outside any graph memory pool),
-// registers it here and launches. Every check and error message is the Python path's, so both raise the same
-// RuntimeError for the same arguments.
+// registers it here and launches. Every attention check and error message is the Python path's, so both raise the
+// same RuntimeError for the same arguments. The GEMVs need no workspace and go through this module alone.
 //
 // The C ABI functions come as addresses (bind), taken from the library the package has already loaded and checked,
 // so this module never loads a second copy of it. Host code only: compiled with g++ against torch's headers.
@@ -21,6 +22,7 @@
 #include <tuple>
 #include <vector>
 
+#include "bz_gemv.h"
 #include "bz_gqa_decode.h"
 
 #ifndef BZ_EAGER_BUILD_ID
@@ -33,11 +35,15 @@ using DecodeFn = int (*)(const bz_gqa_decode_args*, hipStream_t);
 using FusedFn = int (*)(const bz_gqa_decode_fused_args*, hipStream_t);
 using StatusFn = const char* (*)(int);
 using WsSizeFn = int (*)(int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, size_t*);
+using GemvFn = int (*)(const bz_gemv_args*, hipStream_t);
+using RmsnormFn = int (*)(const void*, int64_t, const void*, float, void*, int64_t, int32_t, int32_t, hipStream_t);
 
 DecodeFn g_decode = nullptr, g_masked = nullptr, g_noalloc = nullptr;
 FusedFn g_fused = nullptr;
 StatusFn g_status = nullptr;
 WsSizeFn g_ws_size = nullptr;
+GemvFn g_gemv = nullptr;
+RmsnormFn g_rmsnorm = nullptr;
 
 // (device, raw stream, rows x kv heads) -> the workspace the Python side allocated for that stream
 std::map<std::tuple<int, uintptr_t, int64_t>, at::Tensor> g_ws;
@@ -216,7 +222,7 @@ PyObject* result(PyObject* out_obj, const at::Tensor& out) {
 }
 
 bool bound() {
-  if (g_decode && g_masked && g_noalloc && g_fused && g_status && g_ws_size) return true;
+  if (g_decode && g_masked && g_noalloc && g_fused && g_status && g_ws_size && g_gemv && g_rmsnorm) return true;
   PyErr_SetString(PyExc_RuntimeError, "_bz_eager: bind() has not been called");
   return false;
 }
@@ -380,16 +386,157 @@ PyObject* fused(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   }
 }
 
-// bind(decode, masked, noalloc, fused, status_string, workspace_size): the C ABI functions' addresses
+// ---- the backbone GEMVs (bz_gemv, bz_rmsnorm)
+
+// x: a bf16 [M, K] device tensor, M 1..4, K and the row stride multiples of 8
+void gemv_x(const at::Tensor& x, const char* name, int64_t& M, int64_t& K) {
+  check(x.is_cuda() && x.scalar_type() == at::kBFloat16 && x.dim() == 2 && x.stride(1) == 1,
+        std::string(name) + " must be a bf16 [M, K] device tensor with a contiguous last dim");
+  M = x.size(0), K = x.size(1);
+  check(1 <= M && M <= 4, std::string(name) + ": M must be 1..4, got " + std::to_string(M));
+  check(K % 8 == 0 && x.stride(0) % 8 == 0, std::string(name) + ": K and the row stride must be multiples of 8");
+}
+// a weight: a contiguous bf16 [N, K] device tensor; returns N
+int64_t gemv_w(const at::Tensor& w, int64_t K, const char* name) {
+  check(w.is_cuda() && w.scalar_type() == at::kBFloat16 && w.is_contiguous() && w.dim() == 2 && w.size(1) == K,
+        std::string(name) + " must be a contiguous bf16 [N, " + std::to_string(K) + "] device tensor");
+  return w.size(0);
+}
+// an output or residual: a bf16 [M, N] device tensor with a contiguous last dim
+void gemv_y(const at::Tensor& y, int64_t M, int64_t N, const char* name) {
+  check(y.is_cuda() && y.scalar_type() == at::kBFloat16 && y.dim() == 2 && y.size(0) == M && y.size(1) == N &&
+            y.stride(1) == 1,
+        std::string(name) + " must be a bf16 [" + std::to_string(M) + ", " + std::to_string(N) +
+            "] device tensor with a contiguous last dim");
+}
+void gemv_norm_w(const at::Tensor& nw, int64_t K) {
+  check(nw.is_cuda() && nw.scalar_type() == at::kBFloat16 && nw.is_contiguous() && nw.numel() == K,
+        "the norm weight must be a contiguous bf16 [" + std::to_string(K) + "] device tensor");
+}
+
+// gemv(kind, x, norm_weight, eps, w0, w1, w2, res, y) -> y. kind 0: gemv_seg (norm_weight may be None; w1 / w2 None
+// or empty for absent segments), 1: gemv_resid (w0, res), 2: gemv_gateup (norm_weight, w0 = gate, w1 = up).
+PyObject* gemv(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!bound()) return nullptr;
+  if (nargs != 9) {
+    PyErr_SetString(PyExc_TypeError, "gemv() takes 9 arguments");
+    return nullptr;
+  }
+  try {
+    const long kind = PyLong_AsLong(args[0]);
+    const double eps = PyFloat_AsDouble(args[3]);
+    if (PyErr_Occurred()) return nullptr;
+    const at::Tensor& x = tensor(args[1], "x");
+    const at::Tensor* nw = tensor_or_none(args[2], "norm_weight");
+    const at::Tensor* w[3] = {tensor_or_none(args[4], "W0"), tensor_or_none(args[5], "W1"),
+                              tensor_or_none(args[6], "W2")};
+    const at::Tensor* res = tensor_or_none(args[7], "res");
+    const at::Tensor& y = tensor(args[8], "y");
+    int64_t M, K;
+    gemv_x(x, "x", M, K);
+    bz_gemv_args a{};
+    const char* what;
+    if (kind == 0) {
+      what = "gemv_seg";
+      check(w[0] != nullptr, "W0 must be a tensor");
+      const int64_t n0 = gemv_w(*w[0], K, "W0");
+      const int64_t n1 = w[1] && w[1]->numel() ? gemv_w(*w[1], K, "W1") : 0;
+      const int64_t n2 = w[2] && w[2]->numel() ? gemv_w(*w[2], K, "W2") : 0;
+      gemv_y(y, M, n0 + n1 + n2, "y");
+      a.epilogue = BZ_GEMV_PLAIN;
+      if (nw) {
+        gemv_norm_w(*nw, K);
+        a.norm_weight = nw->data_ptr(), a.eps = (float)eps;
+      }
+      a.w[0] = w[0]->data_ptr(), a.n[0] = (int32_t)n0;
+      if (n1) a.w[1] = w[1]->data_ptr(), a.n[1] = (int32_t)n1;
+      if (n2) a.w[2] = w[2]->data_ptr(), a.n[2] = (int32_t)n2;
+    } else if (kind == 1) {
+      what = "gemv_resid";
+      check(w[0] != nullptr && res != nullptr, "W and res must be tensors");
+      const int64_t n = gemv_w(*w[0], K, "W");
+      gemv_y(*res, M, n, "res");
+      gemv_y(y, M, n, "y");
+      a.epilogue = BZ_GEMV_RESIDUAL;
+      a.w[0] = w[0]->data_ptr(), a.n[0] = (int32_t)n;
+      a.res = res->data_ptr(), a.res_stride = res->stride(0);
+    } else if (kind == 2) {
+      what = "gemv_gateup";
+      check(w[0] != nullptr && w[1] != nullptr && nw != nullptr, "Wg, Wu and the norm weight must be tensors");
+      const int64_t n = gemv_w(*w[0], K, "Wg");
+      check(gemv_w(*w[1], K, "Wu") == n, "Wg and Wu must have the same number of rows");
+      gemv_y(y, M, n, "y");
+      gemv_norm_w(*nw, K);
+      a.epilogue = BZ_GEMV_SILU_MUL;
+      a.norm_weight = nw->data_ptr(), a.eps = (float)eps;
+      a.w[0] = w[0]->data_ptr(), a.w[1] = w[1]->data_ptr();
+      a.n[0] = (int32_t)n, a.n[1] = (int32_t)n;
+    } else {
+      throw Error{"gemv: kind must be 0 (seg), 1 (resid) or 2 (gateup)"};
+    }
+    a.x = x.data_ptr(), a.x_stride = x.stride(0);
+    a.y = y.data_ptr(), a.y_stride = y.stride(0);
+    a.m = (int32_t)M, a.k = (int32_t)K;
+    const int idx = x.device().index();
+    DeviceScope scope(idx);
+    check_status(g_gemv(&a, c10::hip::getCurrentHIPStream(idx).stream()), what);
+    Py_INCREF(args[8]);
+    return args[8];
+  } catch (const Error& e) {
+    PyErr_SetString(PyExc_RuntimeError, e.msg.c_str());
+    return nullptr;
+  } catch (const std::exception& e) {
+    PyErr_SetString(PyExc_RuntimeError, e.what());
+    return nullptr;
+  }
+}
+
+// rmsnorm(x, w, eps, y) -> y: the standalone row RMSNorm
+PyObject* rmsnorm(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!bound()) return nullptr;
+  if (nargs != 4) {
+    PyErr_SetString(PyExc_TypeError, "rmsnorm() takes 4 arguments");
+    return nullptr;
+  }
+  try {
+    const double eps = PyFloat_AsDouble(args[2]);
+    if (PyErr_Occurred()) return nullptr;
+    const at::Tensor& x = tensor(args[0], "x");
+    const at::Tensor& w = tensor(args[1], "w");
+    const at::Tensor& y = tensor(args[3], "y");
+    check(x.is_cuda() && x.scalar_type() == at::kBFloat16 && x.dim() == 2 && x.stride(1) == 1,
+          "x must be a bf16 [M, K] device tensor with a contiguous last dim");
+    const int64_t M = x.size(0), K = x.size(1);
+    gemv_norm_w(w, K);
+    gemv_y(y, M, K, "y");
+    const int idx = x.device().index();
+    DeviceScope scope(idx);
+    check_status(g_rmsnorm(x.data_ptr(), x.stride(0), w.data_ptr(), (float)eps, y.data_ptr(), y.stride(0),
+                           (int32_t)M, (int32_t)K, c10::hip::getCurrentHIPStream(idx).stream()),
+                 "rmsnorm");
+    Py_INCREF(args[3]);
+    return args[3];
+  } catch (const Error& e) {
+    PyErr_SetString(PyExc_RuntimeError, e.msg.c_str());
+    return nullptr;
+  } catch (const std::exception& e) {
+    PyErr_SetString(PyExc_RuntimeError, e.what());
+    return nullptr;
+  }
+}
+
+// bind(decode, masked, noalloc, fused, status_string, workspace_size, gemv, rmsnorm): the C ABI functions' addresses
 PyObject* bind(PyObject*, PyObject* args) {
-  unsigned long long d, m, n, f, s, w;
-  if (!PyArg_ParseTuple(args, "KKKKKK", &d, &m, &n, &f, &s, &w)) return nullptr;
+  unsigned long long d, m, n, f, s, w, g, r;
+  if (!PyArg_ParseTuple(args, "KKKKKKKK", &d, &m, &n, &f, &s, &w, &g, &r)) return nullptr;
   g_decode = reinterpret_cast<DecodeFn>(d);
   g_masked = reinterpret_cast<DecodeFn>(m);
   g_noalloc = reinterpret_cast<DecodeFn>(n);
   g_fused = reinterpret_cast<FusedFn>(f);
   g_status = reinterpret_cast<StatusFn>(s);
   g_ws_size = reinterpret_cast<WsSizeFn>(w);
+  g_gemv = reinterpret_cast<GemvFn>(g);
+  g_rmsnorm = reinterpret_cast<RmsnormFn>(r);
   Py_RETURN_NONE;
 }
 
@@ -415,13 +562,17 @@ PyMethodDef kMethods[] = {
      "gqa_decode / gqa_decode_masked through the C ABI, or None when the stream has no workspace yet"},
     {"fused", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(fused)), METH_FASTCALL,
      "gqa_decode_fused through the C ABI, or None when the stream has no workspace yet"},
+    {"gemv", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(gemv)), METH_FASTCALL,
+     "gemv_seg / gemv_resid / gemv_gateup through the C ABI"},
+    {"rmsnorm", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(rmsnorm)), METH_FASTCALL,
+     "rmsnorm through the C ABI"},
     {"bind", bind, METH_VARARGS, "the C ABI functions' addresses"},
     {"register_workspace", register_workspace, METH_VARARGS, "a workspace made for (device, stream, groups)"},
     {"build_id", build_id, METH_NOARGS, "hash of the sources this module was built from"},
     {nullptr, nullptr, 0, nullptr}};
 
-PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_bz_eager", "native eager binding of the decode-attention entries", -1,
-                       kMethods};
+PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_bz_eager",
+                       "native eager binding of the decode-attention entries and the backbone GEMVs", -1, kMethods};
 
 }  // namespace
 

@@ -297,7 +297,8 @@ def eager():
                            f"hash to {current}): rebuild it (python -c 'import __graft_entry__ as g; g.build()')")
     addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
     mod.bind(addr(lib.bz_gqa_decode), addr(lib.bz_gqa_decode_masked), addr(lib.bz_gqa_decode_noalloc),
-             addr(lib.bz_gqa_decode_fused), addr(lib.bz_status_string), addr(lib.bz_gqa_decode_workspace_size))
+             addr(lib.bz_gqa_decode_fused), addr(lib.bz_status_string), addr(lib.bz_gqa_decode_workspace_size),
+             addr(lib.bz_gemv), addr(lib.bz_rmsnorm))
     with _LOCK:
         if _EAGER is None:
             _EAGER = mod
