@@ -113,7 +113,9 @@ def mi355_decode_attention(module, query: torch.Tensor, key: torch.Tensor, value
         lens = torch.full((B,), key.size(2), dtype=torch.int32, device=query.device)
         gqa_decode(query, key, value, lens, scaling, out)
     else:
-        gqa_decode_masked(query, key, value, attention_mask[:, :, -1:, :], scaling, out)
+        # the query row's mask ([B, 1, 1, S] at decode already: no slicing view to build)
+        mask = attention_mask if attention_mask.size(2) == 1 else attention_mask[:, :, -1:, :]
+        gqa_decode_masked(query, key, value, mask, scaling, out)
     return out, None
 
 
