@@ -159,6 +159,46 @@ def test_block_kernel_segments_and_strides(device, M, K):
     assert_gemv_close(host_bits(y), gemv_ref(xs[:, :K], W, nw, 1e-6), f"segments M={M} K={K}")
 
 
+def _random_block_cases(n=24, seed=2024):
+    """(M, K, N, kind) drawn with a fixed seed from the block kernel's two routes: 4096 < K <= 6144 at any M and
+    1024 < K <= 2048 at M >= 3, K any multiple of 8 in the range, N from 1 to 700."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        if i % 2:
+            M, K = int(rng.integers(1, 5)), 8 * int(rng.integers(4096 // 8 + 1, 6144 // 8 + 1))
+        else:
+            M, K = int(rng.integers(3, 5)), 8 * int(rng.integers(1024 // 8 + 1, 2048 // 8 + 1))
+        cases.append((M, K, int(rng.integers(1, 701)), ["plain", "norm", "residual", "silu"][i % 4]))
+    return cases
+
+
+@pytest.mark.parametrize("M,K,N,kind", _random_block_cases())
+def test_random_block_shapes(device, M, K, N, kind):
+    rng = np.random.default_rng(M * 100003 + K * 7 + N)
+    x = rand_bits(rng, M, K, scale=2.0)
+    W = rand_bits(rng, N, K, scale=K ** -0.5)
+    nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    xd, Wd, nwd = dev_bf16(x, device), dev_bf16(W, device), dev_bf16(nw, device)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+    if kind == "plain":
+        gemv_seg(xd, None, 0.0, Wd, torch.empty(0), torch.empty(0), y)
+        ref = gemv_ref(x, [W])
+    elif kind == "norm":
+        gemv_seg(xd, nwd, 1e-6, Wd, torch.empty(0), torch.empty(0), y)
+        ref = gemv_ref(x, [W], nw, 1e-6)
+    elif kind == "residual":
+        res = rand_bits(rng, M, N)
+        gemv_resid(xd, Wd, dev_bf16(res, device), y)
+        ref = gemv_ref(x, [W], epilogue="residual", res_bits=res)
+    else:
+        Wu = rand_bits(rng, N, K, scale=K ** -0.5)
+        gemv_gateup(xd, nwd, 1e-6, Wd, dev_bf16(Wu, device), y)
+        ref = gemv_ref(x, [W, Wu], nw, 1e-6, epilogue="silu_mul")
+    torch.cuda.synchronize()
+    assert_gemv_close(host_bits(y), ref, f"{kind} M={M} K={K} N={N}", 0.95 if kind == "silu" else 0.98)
+
+
 def test_identity_weights_exact(device):
     # W = I: every output is its x element, bit for bit (one nonzero product per output)
     K = 1024
